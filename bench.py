@@ -1,0 +1,185 @@
+"""Benchmark: Gemma-3-1B-architecture Q8_0 batch-1 greedy decode after a
+2048-token context, on one MI355X, through the C-ABI.
+
+A "step" is one decode token: forward pass over 26 layers + tied LM head +
+greedy selection, with the token read back to the host (one gg_step call, as
+the reference's per-token loop does). Weights are seeded random-init Q8_0 of
+the 1B architecture (no checkpoint is available offline); the KV cache holds
+2048 positions from a step-by-step prefill of seeded ids before timing.
+
+Prints one JSON line. `roofline` covers the dominant kernel, timed inside the
+timed loop by HIP event-record nodes captured around that launch in the
+graph; `cpu_baseline` times the C oracle (a CPU restatement of the reference
+pipeline) on a bounded sample of the same decode steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "webgpu-gemma_amd")]
+
+import numpy as np  # noqa: E402
+
+from gemma_amd import capi, synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Gemma-3-1B Q8_0 bs1 decode tok/s @ctx2k; HBM GB/s as % of peak; prefill TTFT"
+
+
+def step_bytes(shape, pos: int) -> int:
+    """Algorithmic HBM bytes of one decode token at position `pos`: Q8_0
+    weights at 34 B / 32, f32 norm weights, the f32 KV span each layer
+    attends to, the KV row written, and the 1 MiB logits written + read."""
+    H, L = shape.hidden, shape.layers
+    w = shape.q8_bytes()
+    norms = L * 4 * (4 * H + 2 * shape.head_dim) + 4 * H
+    kv = 0
+    for l in range(L):
+        swa = (l % shape.swa_period) < shape.swa_period - 1
+        span = pos + 1 if not (swa and shape.window) else min(shape.window, pos + 1)
+        kv += span * 2 * shape.kv_dim * 4
+    kv_write = L * 2 * shape.kv_dim * 4
+    logits = 2 * shape.vocab * 4
+    return w + norms + kv + kv_write + logits
+
+
+def kernel_bytes(shape, kind: str, pos: int) -> int:
+    """Algorithmic bytes of one launch of the probed kernel (weights at
+    34 B / 32 + f32 input and output vectors)."""
+    H, I, V, Q = shape.hidden, shape.inter, shape.vocab, shape.q_dim
+    nqkv = Q + 2 * shape.kv_dim
+    q8 = lambda rows, k: rows * k // 32 * 34  # noqa: E731
+    if kind == "qkv":
+        return q8(nqkv, H) + 4 * H + 4 * nqkv
+    if kind == "o":
+        return q8(H, Q) + 4 * Q + 4 * H
+    if kind == "gate_up":
+        return q8(2 * I, H) + 4 * H + 4 * I
+    if kind == "down":
+        return q8(H, I) + 4 * I + 4 * H
+    if kind == "lm_head":
+        return q8(V, H) + 4 * H + 4 * V
+    raise ValueError(kind)
+
+
+def cpu_baseline(shape, tensors, pos0: int, budget_s: float, threads: int):
+    from oracle import oracle as orc
+    orc.set_threads(threads)
+    o = orc.OracleModel(shape, tensors)
+    n, t0 = 0, time.perf_counter()
+    tok = 2
+    while True:
+        o.forward(tok, pos0 + n)
+        tok = o.select(0.0, 0.9, 1.0, 0.0)
+        n += 1
+        el = time.perf_counter() - t0
+        if n >= 2 and el >= budget_s:
+            break
+    o.close()
+    return {"value": n / el, "unit": "tok/s", "cores": orc.get_threads(), "kind": "port",
+            "sample": f"{n} greedy decode steps (forward + LM head + argmax) of the 1B shape at positions "
+                      f"{pos0}..{pos0 + n - 1} over a zero-filled KV cache, C oracle with OpenMP over "
+                      f"output rows, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=2048, help="context positions filled before decoding")
+    ap.add_argument("--probe", default="gate_up", choices=["qkv", "o", "gate_up", "down", "lm_head"])
+    ap.add_argument("--probe-layer", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--reference-mode", action="store_true", help="full attention, one theta (src/ as shipped)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the token loop at batch 1 "
+              f"runs on a single MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    ctx_len = max(4096, args.ctx + args.warmup + args.steps + 8)
+    shape = synth.GEMMA3_1B.with_ctx(ctx_len)
+    shape = shape.reference_mode() if args.reference_mode else shape.gemma3_mode()
+    t0 = time.perf_counter()
+    tensors = synth.make_model(shape, seed=1)
+    t_gen = time.perf_counter() - t0
+    e = capi.Engine(shape.gg_config())
+    e.set_probe(args.probe, args.probe_layer)
+    e.upload_model(tensors)
+    e.finalize()
+    print(f"# model ready: generate {t_gen:.1f}s, upload {time.perf_counter() - t0 - t_gen:.1f}s", file=sys.stderr,
+          flush=True)
+
+    prompt = synth.prompt_ids(args.ctx, seed=2048, vocab=shape.vocab)
+    t0 = time.perf_counter()
+    e.prefill(prompt, 0)
+    tok = e.select()
+    prefill_s = time.perf_counter() - t0
+    print(f"# prefill {args.ctx} tokens + first select: {prefill_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
+
+    pos = args.ctx
+    for _ in range(args.warmup):
+        tok = e.step(tok, pos)
+        pos += 1
+    pos_timed0 = pos
+    probe_ms = []
+    fwd_ms = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = e.step(tok, pos)
+        probe_ms.append(e.probe_elapsed_ms())
+        fwd_ms.append(sum(e.last_timing()))
+        pos += 1
+    elapsed = time.perf_counter() - t0
+    e.close()
+
+    value = args.steps / elapsed
+    ms_per_step = elapsed * 1e3 / args.steps
+    avg_bytes = float(np.mean([step_bytes(shape, p) for p in range(pos_timed0, pos)]))
+    k_bytes = kernel_bytes(shape, args.probe, pos_timed0)
+    k_ms = float(np.mean(probe_ms))
+    achieved = k_bytes / (k_ms * 1e-3) / 1e9
+    dev_ms = float(np.mean(fwd_ms))
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded random-init Q8_0 weights of the Gemma-3-1B architecture, seeded uniform ids",
+        "config": {"workload": "gemma3-1b-q8_0-greedy-decode-after-2048", "ctx_prefilled": args.ctx,
+                   "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
+                   "gemma3 (22 local layers window 512 theta 1e4, 4 global theta 1e6)",
+                   "positions": [pos_timed0, pos - 1]},
+        "roofline": {"bound": "hbm", "kernel": f"{args.probe} GEMV (layer {args.probe_layer})",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": k_bytes, "avg_launch_us": round(k_ms * 1e3, 2)},
+        "step_roofline": {"bytes_per_token": int(avg_bytes),
+                          "achieved_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                          "frac": round(avg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "device_ms_per_step": round(dev_ms, 4)},
+        "prefill": {"tokens": args.ctx, "ms": round(prefill_s * 1e3, 1), "mode": "token-by-token (reference)"},
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        try:
+            out["cpu_baseline"] = cpu_baseline(shape, tensors, args.ctx, args.cpu_seconds, threads)
+        except Exception as ex:  # the oracle is optional for the GPU number
+            out["cpu_baseline"] = {"error": str(ex)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

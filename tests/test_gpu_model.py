@@ -1,0 +1,186 @@
+"""Whole token loop on the GPU through the C-ABI against the oracle:
+per-layer hidden states, normed hidden and logits within 1e-3 relative,
+identical greedy and sampled token sequences, and the position/KV-reuse
+properties of the reference's generate() loop (engine.ts:957-1031)."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from gemma_amd import capi, synth
+from oracle import oracle as orc
+
+from gpu_util import rel, say
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+_MODELS = {}
+
+
+def engine(shape, tensors):
+    e = capi.Engine(shape.gg_config())
+    e.upload_model(tensors)
+    e.finalize()
+    return e
+
+
+def check_state(e, o, shape, what=""):
+    for l in range(shape.layers):
+        r = rel(e.read(capi.READ_LAYER_HIDDEN, l), o.buffer(orc.GOR_LAYER_HIDDEN, l))
+        assert r < TOL, f"{what} layer {l} hidden rel {r:.2e}"
+    r = rel(e.read(capi.READ_NORMED), o.buffer(orc.GOR_NORMED))
+    assert r < TOL, f"{what} normed rel {r:.2e}"
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    return synth.make_model(synth.TINY, seed=7)
+
+
+@pytest.mark.parametrize("mode", ["reference", "gemma3"])
+def test_tiny_greedy_loop(gpu, tiny_model, mode):
+    shape = synth.TINY.reference_mode() if mode == "reference" else synth.TINY.gemma3_mode(window=7)
+    say("tiny greedy", mode)
+    e = engine(shape, tiny_model)
+    o = orc.OracleModel(shape, tiny_model)
+    prompt = synth.prompt_ids(9, seed=11, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    check_state(e, o, shape, "prefill")
+    tok = e.select(0.0, 0.9, 1.0, 0.0)
+    assert tok == o.select(0.0, 0.9, 1.0, 0.0)
+    assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL
+    pos = len(prompt)
+    for step in range(24):
+        nxt = e.step(tok, pos, 0.0, 0.9, 1.0, 0.0)
+        o.forward(tok, pos)
+        ref = o.select(0.0, 0.9, 1.0, 0.0)
+        check_state(e, o, shape, f"step {step}")
+        assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL
+        assert nxt == ref, f"step {step}"
+        tok, pos = nxt, pos + 1
+    # the KV cache rows written so far match
+    for l in range(shape.layers):
+        kc = e.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:pos]
+        vc = e.read(capi.READ_V_CACHE, l).reshape(shape.ctx, 256)[:pos]
+        assert rel(kc, o.buffer(orc.GOR_K_CACHE, l).reshape(shape.ctx, 256)[:pos]) < TOL
+        assert rel(vc, o.buffer(orc.GOR_V_CACHE, l).reshape(shape.ctx, 256)[:pos]) < TOL
+    e.close()
+
+
+def test_prefill_equals_steps_and_turns(gpu, tiny_model):
+    shape = synth.TINY.gemma3_mode(window=5)
+    say("prefill vs steps")
+    toks = synth.prompt_ids(17, seed=12, vocab=shape.vocab)
+    a = engine(shape, tiny_model)
+    a.prefill(toks, 0)
+    b = engine(shape, tiny_model)
+    for i, t in enumerate(toks):        # one token per call, positions 0..16
+        b.prefill([t], i)
+    c = engine(shape, tiny_model)       # three turns continuing at kvPosition
+    c.prefill(toks[:4], 0)
+    c.prefill(toks[4:11], 4)
+    c.prefill(toks[11:], 11)
+    ref = a.read(capi.READ_NORMED)
+    assert np.array_equal(b.read(capi.READ_NORMED), ref)
+    assert np.array_equal(c.read(capi.READ_NORMED), ref)
+    for l in range(shape.layers):
+        assert np.array_equal(b.read(capi.READ_K_CACHE, l), a.read(capi.READ_K_CACHE, l))
+    # reset_kv + re-prefill reproduces the same state
+    a.reset_kv()
+    a.prefill(toks, 0)
+    assert np.array_equal(a.read(capi.READ_NORMED), ref)
+    for x in (a, b, c):
+        x.close()
+
+
+def test_tiny_sampling_stream(gpu, tiny_model):
+    # temperature / top-p / repetition penalty with an injected uniform stream
+    shape = synth.TINY.gemma3_mode(window=6)
+    say("tiny sampling")
+    e = engine(shape, tiny_model)
+    o = orc.OracleModel(shape, tiny_model)
+    rng = np.random.default_rng(5)
+    prompt = list(synth.prompt_ids(8, seed=13, vocab=shape.vocab))
+    e.penalty_reset()
+    e.penalty_add(prompt)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    seen = list(prompt)
+    opts = (0.7, 0.9, 1.2)
+    u = float(rng.random())
+    tok = e.select(*opts, u)
+    assert tok == o.select(*opts, u, seen=seen)
+    seen.append(tok)
+    pos = len(prompt)
+    for step in range(30):
+        u = float(rng.random())
+        nxt = e.step(tok, pos, *opts, u)
+        o.forward(tok, pos)
+        assert nxt == o.select(*opts, u, seen=seen), f"step {step}"
+        seen.append(nxt)
+        tok, pos = nxt, pos + 1
+    e.close()
+
+
+def test_270m_greedy_128(gpu):
+    """270M architecture, gemma3 mode: 64 seeded prompt ids then 128 greedy
+    tokens, identical to the oracle; logits within 1e-3 at checkpoints."""
+    shape = synth.GEMMA3_270M.gemma3_mode()
+    say("270m build")
+    t = synth.make_model(shape, seed=270)
+    e = engine(shape, t)
+    o = orc.OracleModel(shape, t)
+    prompt = synth.prompt_ids(64, seed=64, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    check_state(e, o, shape, "prefill")
+    tok = e.select()
+    assert tok == o.select()
+    gpu_toks, ref_toks = [tok], [tok]
+    pos = 64
+    for step in range(127):
+        nxt = e.step(tok, pos)
+        o.forward(tok, pos)
+        ref = o.select()
+        if step % 32 == 0:
+            say("270m step", step)
+            check_state(e, o, shape, f"step {step}")
+            assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL
+        gpu_toks.append(nxt)
+        ref_toks.append(ref)
+        assert nxt == ref, f"token {step + 1} differs"
+        tok, pos = nxt, pos + 1
+    assert len(gpu_toks) == 128
+    e.close()
+
+
+@pytest.mark.parametrize("mode,ctx,span", [("gemma3", 4096, 2048), ("reference", 4096, 2048),
+                                           ("gemma3", 32768, 32768 - 8)])
+def test_1b_full_size_step_with_shared_kv(gpu, mode, ctx, span):
+    """Gemma-3-1B shapes at full size: fill the KV cache on the GPU (step by
+    step prefill of `span` seeded ids), copy it into the oracle, then compare
+    one decode step (per-layer hidden, logits, greedy id) at that position."""
+    shape = synth.GEMMA3_1B.with_ctx(ctx)
+    shape = shape.gemma3_mode() if mode == "gemma3" else shape.reference_mode()
+    say("1b build", mode, ctx, span)
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    e = engine(shape, t)
+    prompt = synth.prompt_ids(span, seed=2048, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    say("1b prefilled")
+    o = orc.OracleModel(shape, t)
+    for l in range(shape.layers):
+        o.buffer(orc.GOR_K_CACHE, l)[:] = e.read(capi.READ_K_CACHE, l)
+        o.buffer(orc.GOR_V_CACHE, l)[:] = e.read(capi.READ_V_CACHE, l)
+    tok = int(prompt[-1])
+    nxt = e.step(tok, span, 0.0, 0.9, 1.0, 0.0)
+    o.forward(tok, span)
+    ref = o.select(0.0, 0.9, 1.0, 0.0)
+    check_state(e, o, shape, "1b step")
+    assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL
+    assert nxt == ref
+    e.close()

@@ -1,0 +1,825 @@
+// gg_runtime.hip -- context, weight upload, captured token graphs and the
+// C-ABI of include/gg.h.
+//
+// Replaces the WebGPU resource layer of GemmaEngineImpl (src/engine.ts:54-110,
+// 124-732, 1039-1077) and drives the gfx950 kernels in gg_kernels.hip.
+// All device memory of a context is allocated in gg_create/gg_finalize; the
+// per-token calls allocate nothing. Per-token work is two captured HIP graphs
+// (forward pass, LM head + selection) that read the token, position and
+// sampling options from a small device struct the host refreshes with one
+// async copy before each launch.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gg.h"
+#include "gg_internal.h"
+
+using namespace gg;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+enum NormIdx { N_ATTN, N_FFN, N_QN, N_KN, N_POST_ATTN, N_POST_FFW, N_NNORM };
+const char* kNormNames[N_NNORM] = {"attn_norm", "ffn_norm", "attn_q_norm", "attn_k_norm",
+                                   "post_attention_norm", "post_ffw_norm"};
+enum Q8Idx { Q_ATTN_Q, Q_ATTN_K, Q_ATTN_V, Q_ATTN_O, Q_GATE, Q_UP, Q_DOWN, Q_NQ8 };
+const char* kQ8Names[Q_NQ8] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+
+struct Layer {
+  uint8_t* qkv = nullptr;   // fused [q | k | v] rows, pair-interleaved
+  uint8_t* o = nullptr;
+  uint8_t* gu = nullptr;    // gate/up rows interleaved 32 + 32 per group
+  uint8_t* down = nullptr;
+  float* norm[N_NNORM] = {};
+  float* kc = nullptr;
+  float* vc = nullptr;
+  uint32_t have = 0;        // bit i: kQ8Names[i]; bit 8 + j: kNormNames[j]
+};
+
+constexpr uint32_t kAllLayerBits = ((1u << Q_NQ8) - 1) | (((1u << N_NNORM) - 1) << 8);
+
+// ceil-division helpers
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// f16 -> f32 (exact; gguf.ts:95-105 semantics, NaN quietened)
+float half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h >> 15) << 31;
+  int ex = (h >> 10) & 0x1f;
+  uint32_t mant = h & 0x3ff;
+  uint32_t bits;
+  if (ex == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      int e = -1;
+      do { mant <<= 1; ++e; } while (!(mant & 0x400));
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((mant & 0x3ff) << 13);
+    }
+  } else if (ex == 31) {
+    bits = mant ? 0x7fc00000u : (sign | 0x7f800000u);
+  } else {
+    bits = sign | ((uint32_t)(ex - 15 + 127) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+}  // namespace
+
+struct gg_ctx {
+  gg_config c{};
+  int H = 0, L = 0, NQ = 0, I = 0, V = 0, CTX = 0, QD = 0, NQKV = 0;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<Layer> layers;
+  uint8_t* embd = nullptr;
+  float* out_norm = nullptr;
+  bool have_embd = false, have_out_norm = false;
+
+  // work buffers
+  float *qkv_part = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_part = nullptr;
+  float *act = nullptr, *down_part = nullptr, *hidden = nullptr, *residual = nullptr, *normed = nullptr;
+  float *logits = nullptr, *hist = nullptr, *q_dbg = nullptr;
+  float *freq_local = nullptr, *freq_global = nullptr;
+  float* cand_val = nullptr;
+  uint32_t *cand_id = nullptr, *top = nullptr, *seen = nullptr;
+  unsigned int* counters = nullptr;   // [0] attention, [1] selector
+  DevState* st = nullptr;
+  int32_t* tokens = nullptr;
+  int32_t* d_ids = nullptr;           // staging for gg_penalty_add
+  uint8_t* staging = nullptr;         // Q8_0 upload staging
+  size_t staging_bytes = 0;
+  int S_qkv = 1, S_o = 1, S_down = 1, CS_qkv = 1, CS_o = 1, CS_down = 1, attn_grid = 1;
+
+  // pinned host mirrors
+  DevState* h_st = nullptr;
+  int32_t* h_tokens = nullptr;
+  int32_t* h_out = nullptr;
+
+  hipGraphExec_t g_fwd = nullptr, g_sel = nullptr;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  int probe_kind = GG_PROBE_NONE, probe_layer = 0;
+  hipEvent_t probe_ev[2] = {nullptr, nullptr};
+  bool probe_done = false;
+  bool finalized = false, lost = false, timed = false;
+  std::vector<void*> allocs;
+  std::string err;
+};
+
+namespace {
+
+int set_err(gg_ctx* c, int code, const std::string& msg) {
+  if (c) c->err = msg;
+  else g_create_error = msg;
+  return code;
+}
+
+// Map a HIP status to a gg code; faults that poison the context are sticky.
+int hip_fail(gg_ctx* c, hipError_t e, const char* what) {
+  std::string m = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  if (c && (e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorECCNotCorrectable ||
+            e == hipErrorLaunchTimeOut || e == hipErrorAssert)) {
+    c->lost = true;
+    return set_err(c, GG_ERR_DEVICE_LOST, "device lost: " + m);
+  }
+  if (e == hipErrorOutOfMemory) return set_err(c, GG_ERR_OOM, m);
+  return set_err(c, GG_ERR_HIP, m);
+}
+
+#define GG_HIP(ctx, call)                                   \
+  do {                                                      \
+    hipError_t e_ = (call);                                 \
+    if (e_ != hipSuccess) return hip_fail((ctx), e_, #call); \
+  } while (0)
+
+template <class T>
+int dalloc(gg_ctx* c, T** p, size_t bytes) {
+  void* v = nullptr;
+  hipError_t e = hipMalloc(&v, bytes ? bytes : 4);
+  if (e != hipSuccess) return hip_fail(c, e, "hipMalloc");
+  c->allocs.push_back(v);
+  *p = (T*)v;
+  return GG_OK;
+}
+
+#define GG_TRY(x)          \
+  do {                     \
+    int r_ = (x);          \
+    if (r_ != GG_OK) return r_; \
+  } while (0)
+
+int launch_rc(gg_ctx* c, int rc, const char* what) {
+  if (rc != 0) return hip_fail(c, (hipError_t)rc, what);
+  return GG_OK;
+}
+
+bool is_swa(const gg_config& c, int il) { return (il % c.swa_period) < (c.swa_period - 1); }
+
+// Column splits of a GEMV: cs pair-columns per block, S blocks per row group.
+void choose_split(int Kp, int cs_target, int* S, int* CS) {
+  int cs = cs_target < Kp ? cs_target : Kp;
+  *S = cdiv(Kp, cs);
+  *CS = cdiv(Kp, *S);
+}
+
+int check_ready(gg_ctx* c) {
+  if (!c) return GG_ERR_INVALID;
+  if (c->lost) return set_err(c, GG_ERR_DEVICE_LOST, "device lost: recreate the context");
+  if (!c->finalized) return set_err(c, GG_ERR_INVALID, "context not finalized");
+  return GG_OK;
+}
+
+// Bracket a launch with external event-record nodes when it is the probe.
+struct ProbeScope {
+  gg_ctx* c;
+  bool on;
+  ProbeScope(gg_ctx* c_, int kind, int layer) : c(c_), on(c_->probe_kind == kind && (layer < 0 || c_->probe_layer == layer)) {
+    if (on) (void)hipEventRecordWithFlags(c->probe_ev[0], c->stream, hipEventRecordExternal);
+  }
+  ~ProbeScope() {
+    if (on) (void)hipEventRecordWithFlags(c->probe_ev[1], c->stream, hipEventRecordExternal);
+  }
+};
+
+GemvArgs gemv_base(const uint8_t* W, int rows, int K, int S, int CS, float* out) {
+  GemvArgs a{};
+  a.W = W;
+  a.Kp = K / 64;
+  a.G = rows / 64;
+  a.S = S;
+  a.CS = CS;
+  a.N = rows;
+  a.out = out;
+  return a;
+}
+
+// Record the forward pass of one token (engine.ts:735-802).
+int record_forward(gg_ctx* c) {
+  const float eps = c->c.rms_norm_eps;
+  for (int l = 0; l < c->L; ++l) {
+    Layer& Ly = c->layers[l];
+    // QKV with the previous layer's post-FFN norm + residual and attn_norm
+    GemvArgs q = gemv_base(Ly.qkv, c->NQKV, c->H, c->S_qkv, c->CS_qkv, c->qkv_part);
+    q.w_pre = Ly.norm[N_ATTN];
+    q.res_out = c->hidden;
+    q.eps = eps;
+    q.st = c->st;
+    q.tokens = c->tokens;
+    {
+    ProbeScope ps(c, GG_PROBE_QKV, l);
+    if (l == 0) {
+      q.embd = c->embd;
+      q.Kp_embd = c->H / 64;
+      q.embed_scale = sqrtf((float)c->H);
+      GG_TRY(launch_rc(c, launch_gemv(PRO_EMBED_NORM, EPI_PARTIAL, q, c->stream), "qkv gemv"));
+    } else {
+      q.pre_part = c->down_part;
+      q.pre_S = c->S_down;
+      q.pre_res = c->residual;
+      q.w_post = c->layers[l - 1].norm[N_POST_FFW];
+      q.hist_out = c->hist + (size_t)(l - 1) * c->H;
+      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_PARTIAL, q, c->stream), "qkv gemv"));
+    }
+    }
+    // attention
+    AttnArgs at{};
+    at.qkv_part = c->qkv_part;
+    at.S = c->S_qkv;
+    at.n_q = c->NQ;
+    at.q_norm = Ly.norm[N_QN];
+    at.k_norm = Ly.norm[N_KN];
+    const bool swa = is_swa(c->c, l);
+    at.freq = swa ? c->freq_local : c->freq_global;
+    at.k_cache = Ly.kc;
+    at.v_cache = Ly.vc;
+    at.window = swa ? c->c.sliding_window : 0;
+    at.eps = eps;
+    at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
+    at.st = c->st;
+    at.part = c->attn_part;
+    at.counter = c->counters;
+    at.attn_out = c->attn_out;
+    at.q_dbg = c->q_dbg + (size_t)l * c->QD;
+    {
+      ProbeScope ps(c, GG_PROBE_ATTN, l);
+      GG_TRY(launch_rc(c, launch_attention(at, c->attn_grid, c->stream), "attention"));
+    }
+    // O projection
+    GemvArgs o = gemv_base(Ly.o, c->H, c->QD, c->S_o, c->CS_o, c->o_part);
+    o.x = c->attn_out;
+    {
+      ProbeScope ps(c, GG_PROBE_O, l);
+      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, o, c->stream), "o gemv"));
+    }
+    // gate/up with post-attn norm + residual + ffn_norm, GeGLU epilogue
+    GemvArgs gu = gemv_base(Ly.gu, 2 * c->I, c->H, 1, c->H / 64, nullptr);
+    gu.pre_part = c->o_part;
+    gu.pre_S = c->S_o;
+    gu.pre_res = c->hidden;
+    gu.w_post = Ly.norm[N_POST_ATTN];
+    gu.w_pre = Ly.norm[N_FFN];
+    gu.res_out = c->residual;
+    gu.eps = eps;
+    gu.act_out = c->act;
+    {
+      ProbeScope ps(c, GG_PROBE_GATE_UP, l);
+      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_GEGLU, gu, c->stream), "gate/up gemv"));
+    }
+    // down projection
+    GemvArgs d = gemv_base(Ly.down, c->H, c->I, c->S_down, c->CS_down, c->down_part);
+    d.x = c->act;
+    {
+      ProbeScope ps(c, GG_PROBE_DOWN, l);
+      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, d, c->stream), "down gemv"));
+    }
+  }
+  FinalArgs f{};
+  f.pre_part = c->down_part;
+  f.pre_S = c->S_down;
+  f.pre_res = c->residual;
+  f.w_post = c->layers[c->L - 1].norm[N_POST_FFW];
+  f.w_out = c->out_norm;
+  f.hidden = c->hidden;
+  f.hist_out = c->hist + (size_t)(c->L - 1) * c->H;
+  f.normed = c->normed;
+  f.H = c->H;
+  f.eps = eps;
+  f.st = c->st;
+  return launch_rc(c, launch_final(f, c->stream), "final norm");
+}
+
+// Record LM head + selection (engine.ts:805-902).
+int record_select(gg_ctx* c) {
+  GemvArgs lm = gemv_base(c->embd, c->V, c->H, 1, c->H / 64, c->logits);
+  lm.x = c->normed;
+  {
+    ProbeScope ps(c, GG_PROBE_LM_HEAD, -1);
+    GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, lm, c->stream), "lm head"));
+  }
+  SelectArgs s{};
+  s.logits = c->logits;
+  s.V = c->V;
+  s.cand_val = c->cand_val;
+  s.cand_id = c->cand_id;
+  s.top = c->top;
+  s.seen = c->seen;
+  s.st = c->st;
+  s.counter = c->counters + 1;
+  s.auto_add = 1;
+  ProbeScope ps(c, GG_PROBE_SELECT, -1);
+  return launch_rc(c, launch_select(s, c->stream), "select");
+}
+
+int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
+  GG_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
+  int rc = rec(c);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rc != GG_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
+  e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(c, e, "hipGraphInstantiate");
+  return GG_OK;
+}
+
+// Copy the host-written head of DevState (everything before seen_count).
+int push_state(gg_ctx* c, size_t from, size_t to) {
+  GG_HIP(c, hipMemcpyAsync((char*)c->st + from, (char*)c->h_st + from, to - from, hipMemcpyHostToDevice,
+                           c->stream));
+  return GG_OK;
+}
+
+int sync(gg_ctx* c, const char* what) {
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, what);
+  return GG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+gg_ctx* gg_create(const gg_config* cfg) {
+  g_create_error.clear();
+  if (!cfg) { set_err(nullptr, GG_ERR_INVALID, "null config"); return nullptr; }
+  const gg_config& k = *cfg;
+  if (k.head_dim != kHeadDim || k.num_kv_heads != 1 || k.num_q_heads < 1 || k.num_q_heads > kMaxQHeads ||
+      k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > kMaxK || k.intermediate_size <= 0 ||
+      k.intermediate_size % 64 || k.intermediate_size > kMaxK || k.vocab_size <= 0 || k.vocab_size % 64 ||
+      k.num_layers <= 0 || k.context_length <= 0 || k.context_length > 32 * kAttnMaxChunks * 8 ||
+      k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK) {
+    set_err(nullptr, GG_ERR_INVALID,
+            "unsupported config: needs head_dim 256, one KV head, <= 8 query heads, hidden/intermediate/vocab "
+            "multiples of 64 (<= 8192 for hidden/intermediate), context <= 65536");
+    return nullptr;
+  }
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+    set_err(nullptr, GG_ERR_NO_DEVICE, "no HIP device found");
+    return nullptr;
+  }
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    set_err(nullptr, GG_ERR_NO_DEVICE, std::string("device is not gfx950 (MI355X): ") + prop.gcnArchName);
+    return nullptr;
+  }
+  gg_ctx* c = new gg_ctx();
+  c->c = k;
+  c->device = dev;
+  c->H = k.hidden_size;
+  c->L = k.num_layers;
+  c->NQ = k.num_q_heads;
+  c->I = k.intermediate_size;
+  c->V = k.vocab_size;
+  c->CTX = k.context_length;
+  c->QD = k.num_q_heads * kHeadDim;
+  c->NQKV = c->QD + 2 * kHeadDim;
+  c->layers.resize(c->L);
+  auto fail = [&](int) -> gg_ctx* {  // argument: the failing gg code
+    g_create_error = c->err;
+    gg_destroy(c);
+    return nullptr;
+  };
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    c->err = "hipStreamCreate failed";
+    return fail(0);
+  }
+  // weights
+  auto q8bytes = [](long long rows, long long K) { return (size_t)(rows * K / 32 * 34); };
+  if (dalloc(c, &c->embd, q8bytes(c->V, c->H)) || dalloc(c, &c->out_norm, (size_t)c->H * 4)) return fail(0);
+  for (Layer& Ly : c->layers) {
+    if (dalloc(c, &Ly.qkv, q8bytes(c->NQKV, c->H)) || dalloc(c, &Ly.o, q8bytes(c->H, c->QD)) ||
+        dalloc(c, &Ly.gu, q8bytes(2LL * c->I, c->H)) || dalloc(c, &Ly.down, q8bytes(c->H, c->I)))
+      return fail(0);
+    for (int j = 0; j < N_NNORM; ++j) {
+      const int n = (j == N_QN || j == N_KN) ? kHeadDim : c->H;
+      if (dalloc(c, &Ly.norm[j], (size_t)n * 4)) return fail(0);
+    }
+  }
+  return c;
+}
+
+int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t* dims, uint32_t ndims,
+                     const void* bytes, size_t nbytes) {
+  if (!c || !name || !bytes || (!dims && ndims)) return set_err(c, GG_ERR_INVALID, "null argument");
+  if (c->lost) return set_err(c, GG_ERR_DEVICE_LOST, "device lost");
+  if (c->finalized) return set_err(c, GG_ERR_INVALID, "upload after gg_finalize");
+  std::string n(name);
+  const std::string suf = ".weight";
+  if (n.size() <= suf.size() || n.compare(n.size() - suf.size(), suf.size(), suf) != 0)
+    return set_err(c, GG_ERR_INVALID, "tensor name must end in .weight: " + n);
+  std::string key = n.substr(0, n.size() - suf.size());
+  int layer = -1;
+  if (key.compare(0, 4, "blk.") == 0) {
+    size_t dot = key.find('.', 4);
+    if (dot == std::string::npos) return set_err(c, GG_ERR_INVALID, "bad tensor name: " + n);
+    layer = atoi(key.substr(4, dot - 4).c_str());
+    if (layer < 0 || layer >= c->L) return set_err(c, GG_ERR_INVALID, "layer out of range: " + n);
+    key = key.substr(dot + 1);
+  }
+  long long d0 = ndims > 0 ? (long long)dims[0] : 0, d1 = ndims > 1 ? (long long)dims[1] : 1;
+  for (uint32_t i = 2; i < ndims; ++i) d1 *= (long long)dims[i];
+
+  // ---- norm vectors (F32 / F16 -> f32) ----
+  float* norm_dst = nullptr;
+  long long norm_n = 0;
+  if (layer < 0 && key == "output_norm") {
+    norm_dst = c->out_norm;
+    norm_n = c->H;
+  } else if (layer >= 0) {
+    for (int j = 0; j < N_NNORM; ++j)
+      if (key == kNormNames[j]) {
+        norm_dst = c->layers[layer].norm[j];
+        norm_n = (j == N_QN || j == N_KN) ? kHeadDim : c->H;
+        c->layers[layer].have |= 1u << (8 + j);
+      }
+  }
+  if (norm_dst) {
+    if (d0 * d1 != norm_n) return set_err(c, GG_ERR_INVALID, "wrong element count for " + n);
+    std::vector<float> f((size_t)norm_n);
+    if (type == GG_TYPE_F32) {
+      if (nbytes != (size_t)norm_n * 4) return set_err(c, GG_ERR_INVALID, "wrong byte count for " + n);
+      memcpy(f.data(), bytes, nbytes);
+    } else if (type == GG_TYPE_F16) {
+      if (nbytes != (size_t)norm_n * 2) return set_err(c, GG_ERR_INVALID, "wrong byte count for " + n);
+      const uint8_t* b = (const uint8_t*)bytes;
+      for (long long i = 0; i < norm_n; ++i) f[i] = half_to_float((uint16_t)(b[2 * i] | (b[2 * i + 1] << 8)));
+    } else {
+      return set_err(c, GG_ERR_INVALID, "norm tensors must be F32 or F16: " + n);
+    }
+    GG_HIP(c, hipMemcpy(norm_dst, f.data(), (size_t)norm_n * 4, hipMemcpyHostToDevice));
+    if (layer < 0) c->have_out_norm = true;
+    return GG_OK;
+  }
+
+  // ---- Q8_0 matrices ----
+  uint8_t* dst = nullptr;
+  long long rows = 0, K = 0, off = 0;
+  int half = 0, bit = -1;
+  if (layer < 0 && key == "token_embd") {
+    dst = c->embd; rows = c->V; K = c->H;
+  } else if (layer >= 0) {
+    Layer& Ly = c->layers[layer];
+    for (int j = 0; j < Q_NQ8; ++j)
+      if (key == kQ8Names[j]) bit = j;
+    switch (bit) {
+      case Q_ATTN_Q: dst = Ly.qkv; rows = c->QD; K = c->H; off = 0; break;
+      case Q_ATTN_K: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD; break;
+      case Q_ATTN_V: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD + kHeadDim; break;
+      case Q_ATTN_O: dst = Ly.o; rows = c->H; K = c->QD; break;
+      case Q_GATE: dst = Ly.gu; rows = c->I; K = c->H; half = 32; off = 0; break;
+      case Q_UP: dst = Ly.gu; rows = c->I; K = c->H; half = 32; off = 32; break;
+      case Q_DOWN: dst = Ly.down; rows = c->H; K = c->I; break;
+      default: break;
+    }
+  }
+  if (!dst) return set_err(c, GG_ERR_INVALID, "unknown tensor: " + n);
+  if (type != GG_TYPE_Q8_0) return set_err(c, GG_ERR_INVALID, "matrix tensors must be Q8_0: " + n);
+  if (ndims != 2 || d0 != K || d1 != rows)
+    return set_err(c, GG_ERR_INVALID, "unexpected shape for " + n);
+  const size_t need = (size_t)(rows * K / 32 * 34);
+  if (nbytes != need) return set_err(c, GG_ERR_INVALID, "wrong byte count for " + n);
+  if (c->staging_bytes < need) {
+    if (c->staging) (void)hipFree(c->staging);
+    c->staging = nullptr;
+    c->staging_bytes = 0;
+    GG_HIP(c, hipMalloc(&c->staging, need));
+    c->staging_bytes = need;
+  }
+  GG_HIP(c, hipMemcpy(c->staging, bytes, need, hipMemcpyHostToDevice));
+  GG_TRY(launch_rc(c, launch_repack(c->staging, dst, rows, (int)(K / 64), off, half, c->stream), "repack"));
+  GG_TRY(sync(c, "repack"));
+  if (layer < 0) c->have_embd = true;
+  else c->layers[layer].have |= 1u << bit;
+  return GG_OK;
+}
+
+int gg_finalize(gg_ctx* c) {
+  if (!c) return GG_ERR_INVALID;
+  if (c->lost) return set_err(c, GG_ERR_DEVICE_LOST, "device lost");
+  if (c->finalized) return GG_OK;
+  if (!c->have_embd) return set_err(c, GG_ERR_MISSING, "missing token_embd.weight");
+  if (!c->have_out_norm) return set_err(c, GG_ERR_MISSING, "missing output_norm.weight");
+  for (int l = 0; l < c->L; ++l)
+    if ((c->layers[l].have & kAllLayerBits) != kAllLayerBits)
+      return set_err(c, GG_ERR_MISSING, "missing tensors of blk." + std::to_string(l));
+  if (c->staging) { (void)hipFree(c->staging); c->staging = nullptr; c->staging_bytes = 0; }
+
+  choose_split(c->H / 64, 4, &c->S_qkv, &c->CS_qkv);
+  choose_split(c->QD / 64, 4, &c->S_o, &c->CS_o);
+  choose_split(c->I / 64, 8, &c->S_down, &c->CS_down);
+  c->attn_grid = std::min(kAttnMaxChunks, cdiv(c->CTX, 32));
+
+  const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
+  for (Layer& Ly : c->layers) {
+    GG_TRY(dalloc(c, &Ly.kc, kvb));
+    GG_TRY(dalloc(c, &Ly.vc, kvb));
+    GG_HIP(c, hipMemset(Ly.kc, 0, kvb));
+    GG_HIP(c, hipMemset(Ly.vc, 0, kvb));
+  }
+  GG_TRY(dalloc(c, &c->qkv_part, (size_t)c->S_qkv * c->NQKV * 4));
+  GG_TRY(dalloc(c, &c->attn_part, (size_t)kAttnMaxChunks * c->NQ * (2 + kHeadDim) * 4));
+  GG_TRY(dalloc(c, &c->attn_out, (size_t)c->QD * 4));
+  GG_TRY(dalloc(c, &c->o_part, (size_t)c->S_o * c->H * 4));
+  GG_TRY(dalloc(c, &c->act, (size_t)c->I * 4));
+  GG_TRY(dalloc(c, &c->down_part, (size_t)c->S_down * c->H * 4));
+  GG_TRY(dalloc(c, &c->hidden, (size_t)c->H * 4));
+  GG_TRY(dalloc(c, &c->residual, (size_t)c->H * 4));
+  GG_TRY(dalloc(c, &c->normed, (size_t)c->H * 4));
+  GG_TRY(dalloc(c, &c->logits, (size_t)c->V * 4));
+  GG_TRY(dalloc(c, &c->hist, (size_t)c->L * c->H * 4));
+  GG_TRY(dalloc(c, &c->q_dbg, (size_t)c->L * c->QD * 4));
+  GG_TRY(dalloc(c, &c->freq_local, (kHeadDim / 2) * 4));
+  GG_TRY(dalloc(c, &c->freq_global, (kHeadDim / 2) * 4));
+  GG_TRY(dalloc(c, &c->cand_val, (size_t)kSelBlocks * 256 * 4));
+  GG_TRY(dalloc(c, &c->cand_id, (size_t)kSelBlocks * 256 * 4));
+  GG_TRY(dalloc(c, &c->top, 512 * 4));
+  GG_TRY(dalloc(c, &c->seen, (size_t)cdiv(c->V, 32) * 4));
+  GG_TRY(dalloc(c, &c->counters, 64));
+  GG_TRY(dalloc(c, &c->st, sizeof(DevState)));
+  GG_TRY(dalloc(c, &c->tokens, (size_t)c->CTX * 4));
+  GG_TRY(dalloc(c, &c->d_ids, (size_t)c->CTX * 4));
+  GG_HIP(c, hipMemset(c->counters, 0, 64));
+  GG_HIP(c, hipMemset(c->st, 0, sizeof(DevState)));
+  GG_HIP(c, hipMemset(c->seen, 0, (size_t)cdiv(c->V, 32) * 4));
+  GG_HIP(c, hipMemset(c->tokens, 0, (size_t)c->CTX * 4));
+  GG_HIP(c, hipMemset(c->attn_out, 0, (size_t)c->QD * 4));
+  GG_HIP(c, hipMemset(c->hidden, 0, (size_t)c->H * 4));
+  GG_HIP(c, hipMemset(c->normed, 0, (size_t)c->H * 4));
+  GG_HIP(c, hipMemset(c->logits, 0, (size_t)c->V * 4));
+
+  // RoPE inverse frequencies, computed once on the host exactly as the WGSL
+  // expression 1.0 / pow(theta, f32(2i) / f32(head_dim)) (shaders.ts:457).
+  float fl[kHeadDim / 2], fg[kHeadDim / 2];
+  for (int i = 0; i < kHeadDim / 2; ++i) {
+    const float e = (float)(i * 2) / (float)kHeadDim;
+    fl[i] = 1.0f / powf(c->c.rope_theta_local, e);
+    fg[i] = 1.0f / powf(c->c.rope_theta_global, e);
+  }
+  GG_HIP(c, hipMemcpy(c->freq_local, fl, sizeof(fl), hipMemcpyHostToDevice));
+  GG_HIP(c, hipMemcpy(c->freq_global, fg, sizeof(fg), hipMemcpyHostToDevice));
+
+  GG_HIP(c, hipHostMalloc((void**)&c->h_st, sizeof(DevState), hipHostMallocDefault));
+  GG_HIP(c, hipHostMalloc((void**)&c->h_tokens, (size_t)c->CTX * 4, hipHostMallocDefault));
+  GG_HIP(c, hipHostMalloc((void**)&c->h_out, 64, hipHostMallocDefault));
+  memset(c->h_st, 0, sizeof(DevState));
+  for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreate(&c->ev[i]));
+  if (c->probe_kind != GG_PROBE_NONE)
+    for (int i = 0; i < 2; ++i) GG_HIP(c, hipEventCreate(&c->probe_ev[i]));
+
+  GG_TRY(capture(c, record_forward, &c->g_fwd));
+  GG_TRY(capture(c, record_select, &c->g_sel));
+  c->finalized = true;
+  return GG_OK;
+}
+
+int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
+  GG_TRY(check_ready(c));
+  if (n < 0 || (n > 0 && !tokens) || start_pos < 0 || (long long)start_pos + n > c->CTX)
+    return set_err(c, GG_ERR_INVALID, "prefill range outside the context");
+  if (n == 0) return GG_OK;
+  for (int i = 0; i < n; ++i) {
+    if (tokens[i] < 0 || tokens[i] >= c->V) return set_err(c, GG_ERR_INVALID, "token id out of range");
+    c->h_tokens[i] = tokens[i];
+  }
+  c->h_st->pos = start_pos;
+  c->h_st->cursor = 0;
+  GG_HIP(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+  GG_TRY(push_state(c, 0, offsetof(DevState, temperature)));
+  for (int i = 0; i < n; ++i) GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
+  c->timed = false;
+  return sync(c, "prefill");
+}
+
+static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bool with_forward) {
+  c->h_st->temperature = s->temperature;
+  c->h_st->top_p = s->top_p;
+  c->h_st->rep_penalty = s->rep_penalty;
+  c->h_st->u = u;
+  if (with_forward) {
+    GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
+    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+    GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
+  } else {
+    GG_TRY(push_state(c, offsetof(DevState, temperature), offsetof(DevState, seen_count)));
+    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+  }
+  GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
+  GG_HIP(c, hipGraphLaunch(c->g_sel, c->stream));
+  GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
+  GG_HIP(c, hipMemcpyAsync(c->h_out, (char*)c->st + offsetof(DevState, out_token), 4, hipMemcpyDeviceToHost,
+                           c->stream));
+  GG_TRY(sync(c, with_forward ? "step" : "select"));
+  c->timed = true;
+  *out = c->h_out[0];
+  return GG_OK;
+}
+
+int gg_select(gg_ctx* c, const gg_sample* s, double u, int32_t* out_token) {
+  GG_TRY(check_ready(c));
+  if (!s || !out_token) return set_err(c, GG_ERR_INVALID, "null argument");
+  return select_impl(c, s, u, out_token, false);
+}
+
+int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u, int32_t* out_token) {
+  GG_TRY(check_ready(c));
+  if (!s || !out_token) return set_err(c, GG_ERR_INVALID, "null argument");
+  if (token < 0 || token >= c->V) return set_err(c, GG_ERR_INVALID, "token id out of range");
+  if (pos < 0 || pos >= c->CTX) return set_err(c, GG_ERR_INVALID, "position outside the context");
+  c->h_tokens[0] = token;
+  c->h_st->pos = pos;
+  c->h_st->cursor = 0;
+  GG_HIP(c, hipMemcpyAsync(c->tokens, c->h_tokens, 4, hipMemcpyHostToDevice, c->stream));
+  return select_impl(c, s, u, out_token, true);
+}
+
+int gg_penalty_reset(gg_ctx* c) {
+  GG_TRY(check_ready(c));
+  GG_HIP(c, hipMemsetAsync(c->seen, 0, (size_t)cdiv(c->V, 32) * 4, c->stream));
+  GG_HIP(c, hipMemsetAsync((char*)c->st + offsetof(DevState, seen_count), 0, 4, c->stream));
+  return sync(c, "penalty reset");
+}
+
+int gg_penalty_add(gg_ctx* c, const int32_t* ids, int32_t n) {
+  GG_TRY(check_ready(c));
+  if (n < 0 || n > c->CTX || (n > 0 && !ids)) return set_err(c, GG_ERR_INVALID, "bad id list");
+  if (n == 0) return GG_OK;
+  for (int i = 0; i < n; ++i) c->h_tokens[i] = ids[i];
+  GG_HIP(c, hipMemcpyAsync(c->d_ids, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+  GG_TRY(launch_rc(c, launch_seen_add(c->seen, c->st, c->d_ids, n, c->V, c->stream), "penalty add"));
+  return sync(c, "penalty add");
+}
+
+int gg_reset_kv(gg_ctx* c) {
+  GG_TRY(check_ready(c));
+  const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
+  for (Layer& Ly : c->layers) {
+    GG_HIP(c, hipMemsetAsync(Ly.kc, 0, kvb, c->stream));
+    GG_HIP(c, hipMemsetAsync(Ly.vc, 0, kvb, c->stream));
+  }
+  return sync(c, "reset kv");
+}
+
+int gg_read(gg_ctx* c, int32_t what, int32_t layer, void* dst, size_t nbytes) {
+  GG_TRY(check_ready(c));
+  if (!dst) return set_err(c, GG_ERR_INVALID, "null destination");
+  const void* src = nullptr;
+  size_t sz = 0;
+  const bool lay_ok = layer >= 0 && layer < c->L;
+  switch (what) {
+    case GG_READ_HIDDEN: src = c->hidden; sz = (size_t)c->H * 4; break;
+    case GG_READ_NORMED: src = c->normed; sz = (size_t)c->H * 4; break;
+    case GG_READ_LOGITS: src = c->logits; sz = (size_t)c->V * 4; break;
+    case GG_READ_TOPK256: src = c->top; sz = 512 * 4; break;
+    case GG_READ_LAYER_HIDDEN:
+      if (!lay_ok) return set_err(c, GG_ERR_INVALID, "layer out of range");
+      src = c->hist + (size_t)layer * c->H; sz = (size_t)c->H * 4; break;
+    case GG_READ_K_CACHE:
+    case GG_READ_V_CACHE:
+      if (!lay_ok) return set_err(c, GG_ERR_INVALID, "layer out of range");
+      src = what == GG_READ_K_CACHE ? c->layers[layer].kc : c->layers[layer].vc;
+      sz = (size_t)c->CTX * kHeadDim * 4; break;
+    case GG_READ_Q:
+      if (!lay_ok) return set_err(c, GG_ERR_INVALID, "layer out of range");
+      src = c->q_dbg + (size_t)layer * c->QD; sz = (size_t)c->QD * 4; break;
+    case GG_READ_ATTN_OUT: src = c->attn_out; sz = (size_t)c->QD * 4; break;
+    default: return set_err(c, GG_ERR_INVALID, "unknown read target");
+  }
+  if (nbytes < sz) sz = nbytes;
+  GG_TRY(sync(c, "read"));
+  GG_HIP(c, hipMemcpy(dst, src, sz, hipMemcpyDeviceToHost));
+  return GG_OK;
+}
+
+int gg_last_timing(gg_ctx* c, float* forward_ms, float* select_ms) {
+  GG_TRY(check_ready(c));
+  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  float a = 0.f, b = 0.f;
+  GG_HIP(c, hipEventElapsedTime(&a, c->ev[0], c->ev[1]));
+  GG_HIP(c, hipEventElapsedTime(&b, c->ev[1], c->ev[2]));
+  if (forward_ms) *forward_ms = a;
+  if (select_ms) *select_ms = b;
+  return GG_OK;
+}
+
+int gg_set_probe(gg_ctx* c, int32_t kind, int32_t layer) {
+  if (!c) return GG_ERR_INVALID;
+  if (c->finalized) return set_err(c, GG_ERR_INVALID, "gg_set_probe must precede gg_finalize");
+  if (kind < GG_PROBE_NONE || kind > GG_PROBE_SELECT || layer < 0 || layer >= c->L)
+    return set_err(c, GG_ERR_INVALID, "bad probe");
+  c->probe_kind = kind;
+  c->probe_layer = layer;
+  return GG_OK;
+}
+
+int gg_probe_elapsed(gg_ctx* c, float* ms) {
+  GG_TRY(check_ready(c));
+  if (c->probe_kind == GG_PROBE_NONE || !ms) return set_err(c, GG_ERR_INVALID, "no probe set");
+  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  GG_HIP(c, hipEventElapsedTime(ms, c->probe_ev[0], c->probe_ev[1]));
+  return GG_OK;
+}
+
+const char* gg_last_error(const gg_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+void gg_destroy(gg_ctx* c) {
+  if (!c) return;
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
+  if (c->g_sel) (void)hipGraphExecDestroy(c->g_sel);
+  for (hipEvent_t e : c->ev)
+    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->probe_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (void* p : c->allocs) (void)hipFree(p);
+  if (c->staging) (void)hipFree(c->staging);
+  if (c->h_st) (void)hipHostFree(c->h_st);
+  if (c->h_tokens) (void)hipHostFree(c->h_tokens);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+// ---- kernel-level entry points --------------------------------------------
+
+int gg_q8_0_repack(const void* src, void* dst, int64_t rows, int64_t k, void* stream) {
+  if (!src || !dst || rows <= 0 || k <= 0 || rows % 64 || k % 64 || k / 64 > (1 << 30)) return GG_ERR_INVALID;
+  const int rc = launch_repack((const uint8_t*)src, (uint8_t*)dst, rows, (int)(k / 64), 0, 0, stream);
+  return rc ? GG_ERR_HIP : GG_OK;
+}
+
+int gg_q8_0_gemv(const void* w, const float* x, float* y, int64_t rows, int64_t k, int32_t splits,
+                 float* workspace, void* stream) {
+  if (!w || !x || !y || rows <= 0 || k <= 0 || rows % 64 || k % 64 || k > kMaxK || rows / 64 > (1 << 24))
+    return GG_ERR_INVALID;
+  const int Kp = (int)(k / 64);
+  int S = 1, CS = Kp;
+  if (splits > 1) {
+    if (!workspace) return GG_ERR_INVALID;
+    choose_split(Kp, cdiv(Kp, splits), &S, &CS);
+  }
+  GemvArgs a = gemv_base((const uint8_t*)w, (int)rows, (int)k, S, CS, S > 1 ? workspace : y);
+  a.x = x;
+  if (launch_gemv(PRO_NONE, EPI_PARTIAL, a, stream)) return GG_ERR_HIP;
+  if (S > 1 && launch_sum_parts(workspace, S, (int)rows, y, stream)) return GG_ERR_HIP;
+  return GG_OK;
+}
+
+int gg_q8_0_dequant(const void* src, float* out, int64_t n, void* stream) {
+  if (!src || !out || n <= 0 || n % 32) return GG_ERR_INVALID;
+  return launch_dequant((const uint8_t*)src, out, n, stream) ? GG_ERR_HIP : GG_OK;
+}
+
+// workspace: DevState | counter | cand_val | cand_id | top | out
+size_t gg_select_workspace_size(int32_t n) {
+  (void)n;
+  return 256 + 64 + (size_t)kSelBlocks * 256 * 8 + 512 * 4 + 64;
+}
+
+int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s, double u,
+                     void* workspace, void* topk_out, int32_t* out_token, void* stream) {
+  if (!logits || n <= 0 || !s || !workspace || !out_token) return GG_ERR_INVALID;
+  hipStream_t hs = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  DevState h{};
+  h.temperature = s->temperature;
+  h.top_p = s->top_p;
+  h.rep_penalty = s->rep_penalty;
+  h.u = u;
+  h.seen_count = seen ? 1 : 0;
+  SelectArgs a{};
+  a.logits = logits;
+  a.V = n;
+  a.st = (DevState*)ws;
+  a.counter = (unsigned int*)(ws + 256);
+  a.cand_val = (float*)(ws + 320);
+  a.cand_id = (uint32_t*)(ws + 320 + (size_t)kSelBlocks * 256 * 4);
+  a.top = topk_out ? (uint32_t*)topk_out : (uint32_t*)(ws + 320 + (size_t)kSelBlocks * 256 * 8);
+  a.seen = seen ? (uint32_t*)seen : (uint32_t*)ws;  // never read when seen_count == 0
+  a.out_token = nullptr;
+  a.auto_add = 0;
+  if (hipMemcpyAsync(ws, &h, sizeof(h), hipMemcpyHostToDevice, hs) != hipSuccess) return GG_ERR_HIP;
+  if (hipMemsetAsync(a.counter, 0, 4, hs) != hipSuccess) return GG_ERR_HIP;
+  if (launch_select(a, hs)) return GG_ERR_HIP;
+  DevState back{};
+  if (hipMemcpyAsync(&back, ws, sizeof(back), hipMemcpyDeviceToHost, hs) != hipSuccess) return GG_ERR_HIP;
+  if (hipStreamSynchronize(hs) != hipSuccess) return GG_ERR_HIP;
+  *out_token = back.out_token;
+  return GG_OK;
+}
+
+}  // extern "C"
