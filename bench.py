@@ -91,7 +91,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=2048, help="context positions filled before decoding")
-    ap.add_argument("--probe", default="gate_up", choices=["qkv", "o", "gate_up", "down", "lm_head"])
+    ap.add_argument("--probe", default="gate_up", choices=["none", "qkv", "o", "gate_up", "down", "lm_head"])
     ap.add_argument("--probe-layer", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -109,7 +109,8 @@ def main():
     tensors = synth.make_model(shape, seed=1)
     t_gen = time.perf_counter() - t0
     e = capi.Engine(shape.gg_config())
-    e.set_probe(args.probe, args.probe_layer)
+    if args.probe != "none":
+        e.set_probe(args.probe, args.probe_layer)
     e.upload_model(tensors)
     e.finalize()
     print(f"# model ready: generate {t_gen:.1f}s, upload {time.perf_counter() - t0 - t_gen:.1f}s", file=sys.stderr,
@@ -132,7 +133,8 @@ def main():
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tok = e.step(tok, pos)
-        probe_ms.append(e.probe_elapsed_ms())
+        if args.probe != "none":
+            probe_ms.append(e.probe_elapsed_ms())
         fwd_ms.append(sum(e.last_timing()))
         pos += 1
     elapsed = time.perf_counter() - t0
@@ -141,8 +143,9 @@ def main():
     value = args.steps / elapsed
     ms_per_step = elapsed * 1e3 / args.steps
     avg_bytes = float(np.mean([step_bytes(shape, p) for p in range(pos_timed0, pos)]))
-    k_bytes = kernel_bytes(shape, args.probe, pos_timed0)
-    k_ms = float(np.mean(probe_ms))
+    probe = args.probe if args.probe != "none" else "gate_up"
+    k_bytes = kernel_bytes(shape, probe, pos_timed0)
+    k_ms = float(np.mean(probe_ms)) if probe_ms else float("nan")
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
     dev_ms = float(np.mean(fwd_ms))
     out = {

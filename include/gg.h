@@ -155,13 +155,17 @@ void gg_destroy(gg_ctx* ctx);
  * These expose single kernels of the path for isolated parity tests and the
  * GEMV benchmark; `stream` is a hipStream_t (NULL = default stream). */
 
-/* Q8_0 GGUF bytes -> the device layout the GEMV reads (same byte count). */
+/* Device bytes of the pair-interleaved layout of a rows x k Q8_0 matrix
+ * (>= the GGUF count rows*k/32*34; 0 for unsupported shapes: rows and k must
+ * be multiples of 64, k <= 8192). */
+size_t gg_q8_0_packed_size(int64_t rows, int64_t k);
+
+/* Q8_0 GGUF bytes -> the device layout the GEMV reads (packQ8_0ForGPU's
+ * role, gguf.ts:126-149, without changing the 34-byte blocks). */
 int gg_q8_0_repack(const void* src_gguf, void* dst, int64_t rows, int64_t k, void* stream);
 
-/* y[rows] = W[rows x k] x[k] on the device layout (linearQ8, shaders.ts:92-151).
- * splits > 1 splits k across blocks and needs workspace of splits*rows f32. */
-int gg_q8_0_gemv(const void* w, const float* x, float* y, int64_t rows, int64_t k, int32_t splits,
-                 float* workspace, void* stream);
+/* y[rows] = W[rows x k] x[k] on the device layout (linearQ8, shaders.ts:92-151). */
+int gg_q8_0_gemv(const void* w, const float* x, float* y, int64_t rows, int64_t k, void* stream);
 
 /* Bit-exact Q8_0 -> f32 (dequantizeQ8_0, gguf.ts:107-124), GGUF blocks in. */
 int gg_q8_0_dequant(const void* src_gguf, float* out, int64_t n_elems, void* stream);

@@ -33,18 +33,16 @@ def test_dequant_bit_exact(gpu):
     assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
 
 
-@pytest.mark.parametrize("k,n", GEMV_SHAPES)
-@pytest.mark.parametrize("splits", [1, 4])
-def test_q8_0_gemv_shapes(gpu, k, n, splits):
-    say("gemv", k, n, splits)
+@pytest.mark.parametrize("k,n", GEMV_SHAPES + [(640, 1536), (2048, 640), (8192, 64), (64, 64)])
+def test_q8_0_gemv_shapes(gpu, k, n):
+    say("gemv", k, n)
     blocks, x = synth.gemv_operands(n, k, seed=k + n)
     src = dev(blocks)
-    w = empty(blocks.nbytes)
+    w = empty(capi.q8_0_packed_size(n, k))
     capi.q8_0_repack(src.data_ptr(), w.data_ptr(), n, k, stream())
     xd = dev(x)
     y = empty(n * 4)
-    ws = empty(max(splits, 1) * n * 4)
-    capi.q8_0_gemv(w.data_ptr(), xd.data_ptr(), y.data_ptr(), n, k, splits, ws.data_ptr(), stream())
+    capi.q8_0_gemv(w.data_ptr(), xd.data_ptr(), y.data_ptr(), n, k, stream())
     got = host(y, np.float32)
     ref = orc.linear_q8(blocks, x, n)
     assert rel(got, ref) < 1e-4
@@ -56,20 +54,28 @@ def test_q8_0_gemv_shapes(gpu, k, n, splits):
         assert np.all(np.abs(got - y64) <= (k + 2) * 2.0 ** -24 * cond)
 
 
-def test_gemv_repack_preserves_bytes(gpu):
-    k, n = 1152, 1536
+@pytest.mark.parametrize("k,n", [(1152, 1536), (1152, 262144 // 16), (6912, 1152)])
+def test_gemv_repack_preserves_bytes(gpu, k, n):
     blocks, _ = synth.gemv_operands(n, k, seed=5)
     src = dev(blocks)
-    w = empty(blocks.nbytes)
+    w = empty(capi.q8_0_packed_size(n, k))
     capi.q8_0_repack(src.data_ptr(), w.data_ptr(), n, k, stream())
     packed = host(w, np.uint8)
-    assert packed.nbytes == n * k // 32 * 34
-    # pair (row r, col c) at ((r//64 * Kp + c) * 64 + r % 64) * 68
+    # pair (row r, col c) at ((g * KpS + c // CI) * 64 + (c % CI) * GR + r % GR) * 68
     kp = k // 64
+    gr = 64 if n >= 8192 else 8
+    ci = 64 // gr
+    kps = -(-kp // ci)
+    assert packed.nbytes == n // gr * kps * 64 * 68
     pairs = blocks.reshape(n, kp, 68)
-    for r, c in [(0, 0), (63, 17), (64, 0), (1000, 5), (n - 1, kp - 1)]:
-        off = ((r // 64 * kp + c) * 64 + r % 64) * 68
+    rng = np.random.default_rng(0)
+    for r, c in [(0, 0), (63, kp - 1), (64, 0), (n - 1, kp - 1)] + [(int(a), int(b)) for a, b in
+                                                                    zip(rng.integers(0, n, 50), rng.integers(0, kp, 50))]:
+        off = ((r // gr * kps + c // ci) * 64 + (c % ci) * gr + r % gr) * 68
         assert np.array_equal(packed[off:off + 68], pairs[r, c])
+    # every GGUF byte appears exactly once: total of all pairs equals the input bytes
+    used = n * kp * 68
+    assert used == blocks.nbytes
 
 
 def _select(logits, seen_ids, T, p, rep, u, want_topk=True):

@@ -3,14 +3,19 @@
 //
 // Device weight layout ("pair-interleaved Q8_0"). A Q8_0 weight matrix with
 // N output rows and K inputs keeps the GGUF 34-byte blocks verbatim (f16 LE
-// scale + 32 int8) but orders them so one wavefront streams contiguous bytes:
+// scale + 32 int8) but orders them so that one wavefront load is 4352
+// contiguous bytes:
 //   * two consecutive blocks of a row form a 68-byte "pair" (64 weights);
-//   * rows are grouped 64 at a time (one row per lane of a wavefront);
+//     Kp = K / 64 pairs per row;
+//   * rows are grouped GR at a time and pair-columns CI at a time, GR * CI =
+//     64 (one pair per lane of a wavefront); a lane l of a wave holds row
+//     l % GR and pair-column offset l / GR of the current column step;
 //   * pair (row r, pair-column c) lives at byte
-//       ((g * Kp + c) * 64 + (r % 64)) * 68,  g = r / 64,  Kp = K / 64.
-// A wavefront that reads pair-column c of group g therefore loads 64 x 68 =
-// 4352 contiguous bytes, every lane's 68 bytes starting on a 4-byte boundary.
-// Byte count is exactly the GGUF count (34 bytes per 32 weights).
+//       ((g * KpS + c / CI) * 64 + (c % CI) * GR + r % GR) * 68,
+//     g = r / GR, KpS = ceil(Kp / CI) column steps per row group.
+// When CI does not divide Kp the last step of each group has unused slots;
+// they are allocated but never read. Every lane's 68 bytes start on a 4-byte
+// boundary, and the bytes read per token are exactly the GGUF count.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -20,11 +25,33 @@ namespace gg {
 constexpr int kHeadDim = 256;        // Gemma-3 270M/1B head_dim
 constexpr int kMaxQHeads = 8;
 constexpr int kPairBytes = 68;
-constexpr int kGroupRows = 64;
-constexpr int kColBytes = kGroupRows * kPairBytes;   // 4352
+constexpr int kColBytes = 64 * kPairBytes;   // one wavefront step: 4352 bytes
 constexpr int kMaxK = 8192;          // largest GEMV input (x staged in LDS)
-constexpr int kSelBlocks = 128;      // stage-1 blocks of the vocab selector
+constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
+constexpr int kAttnChunk = 64;       // base positions per attention block
 constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per token
+
+// Q8_0 matrix in the pair-interleaved layout.
+struct Q8Layout {
+  int rows, K, Kp, CI, GR, KpS;
+  size_t bytes() const { return (size_t)(rows / GR) * KpS * kColBytes; }
+};
+
+// The layout of a matrix: whole 64-row groups (CI = 1) for tall matrices,
+// 8-row groups with 8 pair-columns per step (CI = 8) below 8192 rows, so that
+// even N = 1152 gets 144 blocks without splitting K.
+inline Q8Layout q8_layout(int rows, int K, int force_ci = 0) {
+  Q8Layout L;
+  L.rows = rows;
+  L.K = K;
+  L.Kp = K / 64;
+  const int ci = force_ci ? force_ci : (rows >= 8192 ? 1 : 8);
+  const int gr = 64 / ci;
+  L.GR = gr;
+  L.CI = 64 / gr;
+  L.KpS = (L.Kp + L.CI - 1) / L.CI;
+  return L;
+}
 
 // Per-step scalars the captured graphs read from device memory.
 // The host rewrites the fields before `seen_count` ahead of every launch;
@@ -43,22 +70,19 @@ struct DevState {
 struct GemvArgs {
   const uint8_t* W;     // pair-interleaved weights
   int Kp;               // pairs per row (K / 64)
-  int G;                // row groups (N / 64)
-  int S;                // column splits across blocks
-  int CS;               // pair-columns per split
+  int KpS;              // column steps per row group
   int N;                // output rows
-  float* out;           // [S][N] partial sums (S == 1: the result)
+  float* out;           // [N] result (EPI_OUT)
   const float* x;       // input vector (prologue NONE)
   // prologue inputs (RESID_NORM / EMBED_NORM); the prologue builds x in LDS
-  const float* pre_part;   // [pre_S][K] partial sums of the vector to post-norm
-  int pre_S;
+  const float* pre_vec;    // [K] output of the previous GEMV to post-norm
   const float* pre_res;    // residual stream vector entering the add
-  const float* w_post;     // post-norm weight applied to the summed partials
+  const float* w_post;     // post-norm weight applied to pre_vec
   const float* w_pre;      // pre-norm weight producing x
   float* res_out;          // block 0 writes the new residual stream vector here
   float* hist_out;         // optional second copy (per-layer hidden history)
   const uint8_t* embd;     // pair-interleaved token embedding (EMBED_NORM)
-  int Kp_embd;
+  int embd_KpS;            // its column steps per group (CI = 1)
   const DevState* st;
   const int32_t* tokens;
   float eps;
@@ -67,8 +91,7 @@ struct GemvArgs {
 };
 
 struct AttnArgs {
-  const float* qkv_part;   // [S][n_q*256 + 512] QKV partial sums
-  int S;
+  const float* qkv;        // [n_q*256 + 512] QKV projection output
   int n_q;                 // query heads (one KV head)
   const float* q_norm;     // [256]
   const float* k_norm;     // [256]
@@ -80,13 +103,12 @@ struct AttnArgs {
   float scale;             // 1/sqrt(head_dim)
   const DevState* st;
   float* part;             // [kAttnMaxChunks][n_q][2 + 256]
-  unsigned int* counter;   // arrival counter for the last-block combine
-  float* attn_out;         // [n_q * 256]
+  float* attn_out;         // [n_q * 256] (combine kernel)
   float* q_dbg;            // optional: normed+roped q of this token
 };
 
 struct FinalArgs {
-  const float* pre_part; int pre_S;
+  const float* pre_vec;
   const float* pre_res;
   const float* w_post;
   const float* w_out;
@@ -106,21 +128,18 @@ struct SelectArgs {
   uint32_t* top;           // [256] x {f32 bits, id}: the topk256 layout
   uint32_t* seen;          // [ceil(V/32)] penalty bitmap
   DevState* st;
-  int32_t* out_token;      // optional extra copy
-  unsigned int* counter;
   int auto_add;            // add the chosen id to the bitmap
 };
 
 // ---- launchers (gg_kernels.hip) -------------------------------------------
 enum Prologue { PRO_NONE = 0, PRO_EMBED_NORM = 1, PRO_RESID_NORM = 2 };
-enum Epilogue { EPI_PARTIAL = 0, EPI_GEGLU = 1 };
+enum Epilogue { EPI_OUT = 0, EPI_GEGLU = 1 };
 
-int launch_gemv(int pro, int epi, const GemvArgs& a, void* stream);
-int launch_sum_parts(const float* parts, int S, int N, float* y, void* stream);
+int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream);
 int launch_attention(const AttnArgs& a, int grid, void* stream);
 int launch_final(const FinalArgs& a, void* stream);
 int launch_select(const SelectArgs& a, void* stream);
-int launch_repack(const uint8_t* src, uint8_t* dst, long long rows, int Kp,
+int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,
                   long long dst_row_offset, int interleave_half, void* stream);
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
 int launch_seen_add(uint32_t* seen, DevState* st, const int32_t* ids, int n, int V, void* stream);

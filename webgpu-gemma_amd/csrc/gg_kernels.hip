@@ -1,17 +1,23 @@
 // gg_kernels.hip -- gfx950 (CDNA4) kernels of the Gemma-3 Q8_0 token loop.
 //
-// One forward pass over a token is five kernels per layer:
-//   k_gemv<EMBED_NORM|RESID_NORM, PARTIAL>  fused QKV projection; its prologue
+// One forward pass over a token is six kernels per layer:
+//   k_gemv<EMBED_NORM|RESID_NORM, OUT>  fused QKV projection; its prologue
 //        finishes the previous layer (post-FFN norm + residual) and applies
 //        attn_norm (engine.ts:768-774, 794)
-//   k_attn      QK-norm + RoPE + KV store + split-K decode attention with the
-//               last-arriving block combining the chunks (engine.ts:775-783)
-//   k_gemv<NONE, PARTIAL>       attention output projection (engine.ts:784)
-//   k_gemv<RESID_NORM, GEGLU>   post-attn norm + residual + ffn_norm, gate and
-//               up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
-//   k_gemv<NONE, PARTIAL>       down projection (engine.ts:793)
+//   k_attn          QK-norm + RoPE + KV store + one chunk of decode attention
+//                   per block (engine.ts:775-783)
+//   k_attn_combine  merge of the chunk softmax statistics
+//   k_gemv<NONE, OUT>          attention output projection (engine.ts:784)
+//   k_gemv<RESID_NORM, GEGLU>  post-attn norm + residual + ffn_norm, gate and
+//                   up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
+//   k_gemv<NONE, OUT>          down projection (engine.ts:793)
 // then k_final (post-FFN norm + residual + output_norm, engine.ts:794-801),
-// and for a sampled step the LM head GEMV plus k_select (engine.ts:817-901).
+// and for a sampled step the LM head GEMV plus k_select1/k_select2
+// (engine.ts:817-901).
+//
+// No kernel communicates between its blocks: on this multi-XCD part a
+// device-scope fence is an L2 write-back, so every cross-block dependency is
+// a kernel boundary of the captured graph instead.
 //
 // All arithmetic is fp32 except the int8 weight payload (dequantised exactly
 // in registers) and the sampler's f64 steps, which mirror the JS host's.
@@ -24,6 +30,9 @@
 namespace gg {
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kXPad = 68;          // LDS floats per 64-wide x segment (4 pad: no bank conflicts)
+constexpr int kAttnMaxCh = 256;    // largest attention chunk (positions per block)
 
 // ---------------------------------------------------------------------------
 // helpers
@@ -57,13 +66,6 @@ __device__ __forceinline__ float block_sum256(float v, float* sh4) {
   if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
   __syncthreads();
   return ((sh4[0] + sh4[1]) + sh4[2]) + sh4[3];
-}
-__device__ __forceinline__ float block_max256(float v, float* sh4) {
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(sh4[0], sh4[1]), fmaxf(sh4[2], sh4[3]));
 }
 
 // One 68-byte pair = blocks 2c and 2c+1 of a row: 17 dwords.
@@ -107,15 +109,17 @@ __device__ __forceinline__ float gelu_mul(float x, float up) {
   return g * up;
 }
 
+__device__ __forceinline__ int xs_index(int e) { return (e >> 6) * kXPad + (e & 63); }
+
 // ---------------------------------------------------------------------------
 // GEMV prologues: build the GEMV input x (K floats) in LDS.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float embed_elem(const GemvArgs& a, int token, int e) {
   // shaders.ts:2-23: (f32(q) * scale) * sqrt(f32(H)), row `token` of the
-  // tied embedding, read from the pair-interleaved layout.
+  // tied embedding (layout with CI = 1, GR = 64).
   const int g = token >> 6, ln = token & 63;
   const int b = e >> 5, c = b >> 1;
-  const uint8_t* pr = a.embd + (((size_t)g * a.Kp_embd + c) * 64 + ln) * kPairBytes;
+  const uint8_t* pr = a.embd + (((size_t)g * a.embd_KpS + c) * 64 + ln) * kPairBytes;
   const int off = (b & 1) ? 34 : 0;
   const uint16_t sb = (uint16_t)(pr[off] | (pr[off + 1] << 8));
   const float scale = (float)__builtin_bit_cast(_Float16, sb);
@@ -124,149 +128,191 @@ __device__ __forceinline__ float embed_elem(const GemvArgs& a, int token, int e)
   return t * a.embed_scale;
 }
 
+// Prologue inputs are read into registers before any reduction so that the
+// prologue costs one memory latency, overlapped with the weight stream.
+constexpr int kMaxEPT = kMaxK / 256;   // elements of x per thread
+
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int K, float* sh4) {
   const int tid = threadIdx.x;
+  const int n = (K - tid + 255) / 256;   // elements this thread owns
   if (PRO == PRO_NONE) {
-    for (int e = tid; e < K; e += 256) xs[e] = a.x[e];
+    float xv[kMaxEPT];
+#pragma unroll
+    for (int i = 0; i < kMaxEPT; ++i)
+      if (i < n) xv[i] = a.x[tid + 256 * i];
+#pragma unroll
+    for (int i = 0; i < kMaxEPT; ++i)
+      if (i < n) xs[xs_index(tid + 256 * i)] = xv[i];
     return;
   }
+  float r[kMaxEPT / 4], wp[kMaxEPT / 4];  // K <= 2048 for the norm prologues
   float ss = 0.f;
   if (PRO == PRO_EMBED_NORM) {
     const int token = a.tokens[a.st->cursor];
-    for (int e = tid; e < K; e += 256) {
-      const float h = embed_elem(a, token, e);
-      xs[e] = h;
-      ss = fmaf(h, h, ss);
-      if (blockIdx.x == 0) a.res_out[e] = h;
-    }
-  } else {  // PRO_RESID_NORM: res = pre_res + norm(sum(parts)) * w_post
-    float s1 = 0.f;
-    for (int e = tid; e < K; e += 256) {
-      float v = 0.f;
-      for (int p = 0; p < a.pre_S; ++p) v += a.pre_part[(size_t)p * K + e];
-      xs[e] = v;
-      s1 = fmaf(v, v, s1);
-    }
-    const float ss1 = block_sum256(s1, sh4);
-    const float rms1 = sqrtf(ss1 / (float)K + a.eps);
-    for (int e = tid; e < K; e += 256) {
-      const float t = (xs[e] * a.w_post[e]) / rms1;   // fusedNormAdd, shaders.ts:415
-      const float r = a.pre_res[e] + t;
-      xs[e] = r;
-      ss = fmaf(r, r, ss);
-      if (blockIdx.x == 0) {
-        a.res_out[e] = r;
-        if (a.hist_out) a.hist_out[e] = r;
+#pragma unroll
+    for (int i = 0; i < kMaxEPT / 4; ++i)
+      if (i < n) {
+        const int e = tid + 256 * i;
+        r[i] = embed_elem(a, token, e);
+        wp[i] = a.w_pre[e];
       }
-    }
+#pragma unroll
+    for (int i = 0; i < kMaxEPT / 4; ++i)
+      if (i < n) {
+        ss = fmaf(r[i], r[i], ss);
+        if (blockIdx.x == 0) a.res_out[tid + 256 * i] = r[i];
+      }
+  } else {  // PRO_RESID_NORM: res = pre_res + norm(pre_vec) * w_post
+    float v[kMaxEPT / 4], res[kMaxEPT / 4], wq[kMaxEPT / 4];
+#pragma unroll
+    for (int i = 0; i < kMaxEPT / 4; ++i)
+      if (i < n) {
+        const int e = tid + 256 * i;
+        v[i] = a.pre_vec[e];
+        res[i] = a.pre_res[e];
+        wq[i] = a.w_post[e];
+        wp[i] = a.w_pre[e];
+      }
+    float s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxEPT / 4; ++i)
+      if (i < n) s1 = fmaf(v[i], v[i], s1);
+    const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)K + a.eps);
+#pragma unroll
+    for (int i = 0; i < kMaxEPT / 4; ++i)
+      if (i < n) {
+        const float t = (v[i] * wq[i]) / rms1;   // fusedNormAdd, shaders.ts:415
+        r[i] = res[i] + t;
+        ss = fmaf(r[i], r[i], ss);
+        if (blockIdx.x == 0) {
+          a.res_out[tid + 256 * i] = r[i];
+          if (a.hist_out) a.hist_out[tid + 256 * i] = r[i];
+        }
+      }
   }
-  const float ss2 = block_sum256(ss, sh4);
-  const float rms = sqrtf(ss2 / (float)K + a.eps);       // rmsNorm, shaders.ts:50-53
-  for (int e = tid; e < K; e += 256) xs[e] = (xs[e] * a.w_pre[e]) / rms;
+  const float rms = sqrtf(block_sum256(ss, sh4) / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
+#pragma unroll
+  for (int i = 0; i < kMaxEPT / 4; ++i)
+    if (i < n) xs[xs_index(tid + 256 * i)] = (r[i] * wp[i]) / rms;
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 dequant-GEMV. Block = 256 threads = 4 wavefronts on one 64-row group;
-// the block's pair-columns [c0, c1) are dealt round-robin to the waves, each
-// lane owns one row. blockIdx.x = g * S + s.
+// Q8_0 dequant-GEMV. Block = 256 threads = 4 wavefronts on one group of GR
+// rows; lane l holds row l % GR and pair-column phase l / GR. Wave w takes
+// column steps w, w+4, ...; each step is one 4352-byte contiguous load per
+// wave. Up to kStepsInFlight steps per wave are issued at kernel entry,
+// before the prologue (weights never depend on x), so a launch costs about
+// one memory latency; longer rows continue with a two-step prefetch.
 // ---------------------------------------------------------------------------
-template <int PRO, int EPI>
+template <int PRO, int EPI, int CI, int kStepsInFlight>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  constexpr int GR = 64 / CI;
   extern __shared__ float xs[];
-  __shared__ float red[4][64];
+  __shared__ float red[4][GR];
   __shared__ float sh4[4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int g = blockIdx.x / a.S, s = blockIdx.x - g * a.S;
-  const int c0 = s * a.CS;
-  const int c1 = min(c0 + a.CS, a.Kp);
-  const int K = a.Kp * 64;
-  const uint8_t* base = a.W + ((size_t)g * a.Kp * 64 + lane) * kPairBytes;
+  const int g = blockIdx.x;
+  const int cp = lane / GR;
+  const int Kp = a.Kp, KpS = a.KpS;
+  const uint8_t* base = a.W + ((size_t)g * KpS * 64 + lane) * kPairBytes;
 
-  // Weights do not depend on x: start streaming before the prologue.
-  int c = c0 + wv;
-  Pair cur;
-  if (c < c1) load_pair(base + (size_t)c * kColBytes, cur);
+  Pair st[kStepsInFlight];
+#pragma unroll
+  for (int i = 0; i < kStepsInFlight; ++i) {
+    const int s = wv + 4 * i;
+    if (s < KpS && s * CI + cp < Kp) load_pair(base + (size_t)s * kColBytes, st[i]);
+  }
 
-  gemv_prologue<PRO>(a, xs, K, sh4);
+  gemv_prologue<PRO>(a, xs, Kp * 64, sh4);
   __syncthreads();
 
   float acc = 0.f;
-  for (; c < c1; c += 4) {
-    const int cn = min(c + 4, c1 - 1);
-    Pair nxt;
-    load_pair(base + (size_t)cn * kColBytes, nxt);
-    acc = dot_pair(cur, xs + c * 64, acc);
-    cur = nxt;
+#pragma unroll
+  for (int i = 0; i < kStepsInFlight; ++i) {
+    const int s = wv + 4 * i;
+    const int c = s * CI + cp;
+    if (s < KpS && c < Kp) acc = dot_pair(st[i], xs + c * kXPad, acc);
   }
-  red[wv][lane] = acc;
+  int s = wv + 4 * kStepsInFlight;
+  if (s < KpS) {
+    Pair cur, nxt;
+    if (s * CI + cp < Kp) load_pair(base + (size_t)s * kColBytes, cur);
+    if (s + 4 < KpS && (s + 4) * CI + cp < Kp) load_pair(base + (size_t)(s + 4) * kColBytes, nxt);
+    for (; s < KpS; s += 4) {
+      Pair nn;
+      const int s3 = s + 8;
+      if (s3 < KpS && s3 * CI + cp < Kp) load_pair(base + (size_t)s3 * kColBytes, nn);
+      const int c = s * CI + cp;
+      if (c < Kp) acc = dot_pair(cur, xs + c * kXPad, acc);
+      cur = nxt;
+      nxt = nn;
+    }
+  }
+  // the CI column phases of a row sit in lanes r, r+GR, ...: butterfly sum
+#pragma unroll
+  for (int m = GR; m < 64; m <<= 1) acc += __shfl_xor(acc, m, 64);
+  if (lane < GR) red[wv][lane] = acc;
   __syncthreads();
   if (wv != 0) return;
-  const float r = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-  const int row = g * 64 + lane;
-  if (EPI == EPI_PARTIAL) {
-    a.out[(size_t)s * a.N + row] = r;
+  const float r = lane < GR ? ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane] : 0.f;
+  if (EPI == EPI_OUT) {
+    if (lane < GR) a.out[g * GR + lane] = r;
   } else {
-    // rows 32g'+i (gate) sit in lanes 0..31, the matching up rows in 32..63
-    const float up = __shfl(r, lane + 32, 64);
-    if (lane < 32) a.act_out[g * 32 + lane] = gelu_mul(r, up);
+    // gate rows g*GR/2 + i sit in lanes 0..GR/2-1, the matching up rows in GR/2..GR-1
+    const float up = __shfl(r, lane + GR / 2, 64);
+    if (lane < GR / 2) a.act_out[g * (GR / 2) + lane] = gelu_mul(r, up);
   }
 }
 
-__global__ __launch_bounds__(256) void k_sum_parts(const float* __restrict__ parts, int S, int N,
-                                                   float* __restrict__ y) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= N) return;
-  float v = 0.f;
-  for (int p = 0; p < S; ++p) v += parts[(size_t)p * N + i];
-  y[i] = v;
+// ---------------------------------------------------------------------------
+// Decode attention (one KV head, head_dim 256), one chunk of positions per
+// block. Block b covers [t0, t1) of the attended span [t_lo, pos]; the chunk
+// grows with the span so at most kAttnMaxChunks blocks are live. Every block
+// rebuilds q/k from the QKV output with the per-head RMSNorm + NEOX RoPE
+// (fusedPerHeadNormRope, shaders.ts:420-467); the block holding `pos` stores
+// k/v into the cache (kvCacheStore, shaders.ts:209-227) and reads them from
+// LDS. Scores/softmax/weighted-V follow shaders.ts:229-325 within the chunk
+// and leave (max, sum, o) per head for k_attn_combine.
+//
+// Scores: wave w takes P = 64/NQP positions at a time with one float4 of the
+// head per lane; the P*NQP = 64 partial dots per lane are finished by one
+// reduce-scatter butterfly (63 shuffles) after which lane l owns dot l.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void attn_span(const AttnArgs& a, int pos, int* t_lo, int* ch, int* nch) {
+  const int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
+  const int span = pos - lo + 1;
+  const int c = kAttnChunk * ((span + kAttnChunk * kAttnMaxChunks - 1) / (kAttnChunk * kAttnMaxChunks));
+  *t_lo = lo;
+  *ch = c;
+  *nch = (span + c - 1) / c;
 }
 
-// ---------------------------------------------------------------------------
-// Decode attention (one KV head, head_dim 256).
-// Block b covers positions [t0, t1) of the attended span [t_lo, pos]; the
-// chunk size grows with the span so at most kAttnMaxChunks blocks are live.
-// Every block rebuilds q/k/v from the QKV partials and applies the per-head
-// RMSNorm + NEOX RoPE itself (fusedPerHeadNormRope, shaders.ts:420-467); the
-// block holding `pos` also stores k/v into the cache (kvCacheStore,
-// shaders.ts:209-227). Scores/softmax/weighted-V follow shaders.ts:229-325
-// per chunk; the last block to finish merges the chunks with the usual
-// max-rescaled sums.
-// ---------------------------------------------------------------------------
-constexpr int kAttnMaxCh = 256;
-
+template <int NQP>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
-  __shared__ float qs[kMaxQHeads][kHeadDim];
+  constexpr int P = 64 / NQP;
+  __shared__ float qs[NQP][kHeadDim];
   __shared__ float ks[kHeadDim];
   __shared__ float vs[kHeadDim];
-  __shared__ float sc[kMaxQHeads][kAttnMaxCh];
-  __shared__ float mh[kMaxQHeads], lh[kMaxQHeads];
-  __shared__ float fac[kAttnMaxChunks];
-  __shared__ float sh4[4];
-  __shared__ int is_last;
+  __shared__ float pw[4][64];
+  __shared__ float wm[4][NQP], wl[4][NQP];
+  __shared__ float wo[4][NQP][kHeadDim];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
   const int pos = a.st->pos;
-  const int t_lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
-  const int span = pos - t_lo + 1;
-  const int ch = 32 * ((span + 32 * kAttnMaxChunks - 1) / (32 * kAttnMaxChunks));
-  const int nch = (span + ch - 1) / ch;
+  int t_lo, ch, nch;
+  attn_span(a, pos, &t_lo, &ch, &nch);
   const int b = blockIdx.x;
   if (b >= nch) return;
   const int t0 = t_lo + b * ch;
   const int t1 = min(t0 + ch, pos + 1);
 
-  // 1. q, k, v = sum of the QKV partials
+  // 1. q, k, v from the QKV output (query heads beyond n_q are zero)
   const int nqd = nq * kHeadDim;
-  const int nel = nqd + 2 * kHeadDim;
-  for (int e = tid; e < nel; e += 256) {
-    float v = 0.f;
-    for (int p = 0; p < a.S; ++p) v += a.qkv_part[(size_t)p * nel + e];
-    if (e < nqd) qs[e >> 8][e & 255] = v;
-    else if (e < nqd + kHeadDim) ks[e - nqd] = v;
-    else vs[e - nqd - kHeadDim] = v;
-  }
+  for (int e = tid; e < NQP * kHeadDim; e += 256) qs[e >> 8][e & 255] = e < nqd ? a.qkv[e] : 0.f;
+  ks[tid] = a.qkv[nqd + tid];
+  vs[tid] = a.qkv[nqd + kHeadDim + tid];
   __syncthreads();
 
   // 2. per-head RMSNorm (q heads, then the k head)
@@ -304,96 +350,177 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   if (b == 0 && a.q_dbg)
     for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = qs[e >> 8][e & 255];
 
-  // 4. scores: wave w takes positions t0+w, t0+w+4, ...; lane holds 4 dims
-  float4 q4[kMaxQHeads];
+  // 4. per-wave online softmax over passes of P positions; lane holds 4 dims
+  float4 q4[NQP];
 #pragma unroll
-  for (int h = 0; h < kMaxQHeads; ++h)
-    q4[h] = (h < nq) ? *(const float4*)&qs[h][4 * lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int t = t0 + wv; t < t1; t += 4) {
-    float4 k4;
-    if (t == pos) k4 = *(const float4*)&ks[4 * lane];
-    else k4 = *(const float4*)(a.k_cache + (size_t)t * kHeadDim + 4 * lane);
+  for (int h = 0; h < NQP; ++h) q4[h] = *(const float4*)&qs[h][4 * lane];
+  float m[NQP], l[NQP];
+  float4 o4[NQP];
 #pragma unroll
-    for (int h = 0; h < kMaxQHeads; ++h) {
-      if (h < nq) {
-        float d = q4[h].x * k4.x;
-        d = fmaf(q4[h].y, k4.y, d);
-        d = fmaf(q4[h].z, k4.z, d);
-        d = fmaf(q4[h].w, k4.w, d);
-        d = wave_sum(d);
-        if (lane == 0) sc[h][t - t0] = d * a.scale;
+  for (int h = 0; h < NQP; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+    o4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int my_h = lane % NQP;
+  for (int tb = t0 + wv * P; tb < t1; tb += 4 * P) {
+    float4 kr[P], vr[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int t = tb + i;
+      if (t < pos) {
+        kr[i] = *(const float4*)(a.k_cache + (size_t)t * kHeadDim + 4 * lane);
+        vr[i] = *(const float4*)(a.v_cache + (size_t)t * kHeadDim + 4 * lane);
+      } else if (t == pos) {
+        kr[i] = *(const float4*)&ks[4 * lane];
+        vr[i] = *(const float4*)&vs[4 * lane];
+      } else {
+        kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        vr[i] = kr[i];
       }
     }
-  }
-  __syncthreads();
-
-  // 5. chunk softmax statistics
-  const int n = t1 - t0;
-  for (int h = wv; h < nq; h += 4) {
-    float m = -INFINITY;
-    for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[h][j]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int j = lane; j < n; j += 64) {
-      const float p = expf(sc[h][j] - m);
-      sc[h][j] = p;
-      l += p;
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+#pragma unroll
+      for (int h = 0; h < NQP; ++h) {
+        float d = q4[h].x * kr[i].x;
+        d = fmaf(q4[h].y, kr[i].y, d);
+        d = fmaf(q4[h].z, kr[i].z, d);
+        d = fmaf(q4[h].w, kr[i].w, d);
+        v[i * NQP + h] = d;
+      }
+    // reduce-scatter: afterwards lane l owns the full dot of index l
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      const bool hi = (lane & msk) != 0;
+#pragma unroll
+      for (int i = 0; i < msk; ++i) {
+        const float send = hi ? v[i] : v[i + msk];
+        const float keep = hi ? v[i + msk] : v[i];
+        v[i] = keep + __shfl_xor(send, msk, 64);
+      }
     }
-    l = wave_sum(l);
-    if (lane == 0) { mh[h] = m; lh[h] = l; }
+    const bool valid = tb + lane / NQP < t1 && my_h < nq;
+    const float sco = valid ? v[0] * a.scale : -INFINITY;
+    // pass maximum of head my_h over the lanes holding that head
+    float mx = sco;
+#pragma unroll
+    for (int msk = NQP; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+    float alpha[NQP], m_own = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < NQP; ++h) {
+      const float mn = fmaxf(m[h], __shfl(mx, h, 64));
+      alpha[h] = (m[h] == -INFINITY) ? 0.f : expf(m[h] - mn);
+      m[h] = mn;
+      if (h == my_h) m_own = mn;
+    }
+    const float p = valid ? expf(sco - m_own) : 0.f;
+    float ps = p;
+#pragma unroll
+    for (int msk = NQP; msk < 64; msk <<= 1) ps += __shfl_xor(ps, msk, 64);
+    pw[wv][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int h = 0; h < NQP; ++h) {
+      l[h] = fmaf(l[h], alpha[h], __shfl(ps, h, 64));
+      o4[h].x *= alpha[h];
+      o4[h].y *= alpha[h];
+      o4[h].z *= alpha[h];
+      o4[h].w *= alpha[h];
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+#pragma unroll
+      for (int h = 0; h < NQP; ++h) {
+        const float pp = pw[wv][i * NQP + h];
+        o4[h].x = fmaf(pp, vr[i].x, o4[h].x);
+        o4[h].y = fmaf(pp, vr[i].y, o4[h].y);
+        o4[h].z = fmaf(pp, vr[i].z, o4[h].z);
+        o4[h].w = fmaf(pp, vr[i].w, o4[h].w);
+      }
+    __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
 
-  // 6. o[h][d] = sum_t p[h][t] * V[t][d]; thread = dimension
-  float acc[kMaxQHeads];
+  // 5. merge the four waves (fixed order) into this chunk's (max, sum, o)
+  if (lane < NQP) {
+    float mm = m[0], ll = l[0];
 #pragma unroll
-  for (int h = 0; h < kMaxQHeads; ++h) acc[h] = 0.f;
-  for (int t = t0; t < t1; ++t) {
-    const float v = (t == pos) ? vs[tid] : a.v_cache[(size_t)t * kHeadDim + tid];
-#pragma unroll
-    for (int h = 0; h < kMaxQHeads; ++h)
-      if (h < nq) acc[h] = fmaf(sc[h][t - t0], v, acc[h]);
+    for (int h = 1; h < NQP; ++h)
+      if (lane == h) { mm = m[h]; ll = l[h]; }
+    wm[wv][lane] = mm;
+    wl[wv][lane] = ll;
   }
+#pragma unroll
+  for (int h = 0; h < NQP; ++h) *(float4*)&wo[wv][h][4 * lane] = o4[h];
+  __syncthreads();
   const size_t pstride = (size_t)nq * (2 + kHeadDim);
   float* mypart = a.part + (size_t)b * pstride;
-#pragma unroll
-  for (int h = 0; h < kMaxQHeads; ++h)
-    if (h < nq) mypart[h * (2 + kHeadDim) + 2 + tid] = acc[h];
-  if (tid < nq) {
-    mypart[tid * (2 + kHeadDim)] = mh[tid];
-    mypart[tid * (2 + kHeadDim) + 1] = lh[tid];
-  }
-
-  // 7. the last block to arrive merges all chunks
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned int old =
-        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (old == (unsigned int)(nch - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
   for (int h = 0; h < nq; ++h) {
-    float m = -INFINITY;
-    for (int cc = tid; cc < nch; cc += 256) m = fmaxf(m, a.part[(size_t)cc * pstride + h * (2 + kHeadDim)]);
-    const float M = block_max256(m, sh4);
-    float l = 0.f;
-    for (int cc = tid; cc < nch; cc += 256) {
-      const float* pp = a.part + (size_t)cc * pstride + h * (2 + kHeadDim);
-      const float f = expf(pp[0] - M);
-      fac[cc] = f;
-      l = fmaf(f, pp[1], l);
+    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
+      L = fmaf(f, wl[w][h], L);
+      O = fmaf(f, wo[w][h][tid], O);
     }
-    const float L = block_sum256(l, sh4);   // barrier also publishes fac[]
-    float o = 0.f;
-    for (int cc = 0; cc < nch; ++cc)
-      o = fmaf(fac[cc], a.part[(size_t)cc * pstride + h * (2 + kHeadDim) + 2 + tid], o);
-    a.attn_out[h * kHeadDim + tid] = o / L;
-    __syncthreads();
+    mypart[h * (2 + kHeadDim) + 2 + tid] = O;
+    if (tid == 0) {
+      mypart[h * (2 + kHeadDim)] = M;
+      mypart[h * (2 + kHeadDim) + 1] = L;
+    }
   }
-  if (tid == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the chunk statistics: block = (head, quarter of the head dims).
+// Loads of all chunk statistics and outputs are issued before any arithmetic.
+__global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
+  __shared__ float fac[kAttnMaxChunks];
+  const int lane = threadIdx.x;
+  const int h = blockIdx.x >> 2, d = (blockIdx.x & 3) * 64 + lane;
+  const int pos = a.st->pos;
+  int t_lo, ch, nch;
+  attn_span(a, pos, &t_lo, &ch, &nch);
+  const size_t pstride = (size_t)a.n_q * (2 + kHeadDim);
+  const float* ph = a.part + h * (2 + kHeadDim);
+  float mc[kAttnMaxChunks / 64], lc[kAttnMaxChunks / 64];
+#pragma unroll
+  for (int i = 0; i < kAttnMaxChunks / 64; ++i) {
+    const int c = lane + 64 * i;
+    mc[i] = c < nch ? ph[c * pstride] : -INFINITY;
+    lc[i] = c < nch ? ph[c * pstride + 1] : 0.f;
+  }
+  float o = 0.f, L = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += 32) {
+    float ov[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) ov[k] = c0 + k < nch ? ph[(c0 + k) * pstride + 2 + d] : 0.f;
+    if (c0 == 0) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kAttnMaxChunks / 64; ++i) m = fmaxf(m, mc[i]);
+      const float M = wave_max(m);
+      float l = 0.f;
+#pragma unroll
+      for (int i = 0; i < kAttnMaxChunks / 64; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nch) {
+          const float f = expf(mc[i] - M);
+          fac[c] = f;
+          l = fmaf(f, lc[i], l);
+        }
+      }
+      L = wave_sum(l);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (c0 + k < nch) o = fmaf(fac[c0 + k], ov[k], o);
+  }
+  a.attn_out[h * kHeadDim + d] = o / L;
 }
 
 // ---------------------------------------------------------------------------
@@ -401,27 +528,38 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 // normed = rmsNorm(hidden, output_norm) (engine.ts:794-801); advance pos.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
-  extern __shared__ float hs[];
   __shared__ float sh4[4];
   const int tid = threadIdx.x, H = a.H;
+  const int n = (H - tid + 255) / 256;
+  float v[8], res[8], wq[8], wo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+      const int e = tid + 256 * i;
+      v[i] = a.pre_vec[e];
+      res[i] = a.pre_res[e];
+      wq[i] = a.w_post[e];
+      wo[i] = a.w_out[e];
+    }
   float s1 = 0.f;
-  for (int e = tid; e < H; e += 256) {
-    float v = 0.f;
-    for (int p = 0; p < a.pre_S; ++p) v += a.pre_part[(size_t)p * H + e];
-    hs[e] = v;
-    s1 = fmaf(v, v, s1);
-  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) s1 = fmaf(v[i], v[i], s1);
   const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
   float s2 = 0.f;
-  for (int e = tid; e < H; e += 256) {
-    const float r = a.pre_res[e] + (hs[e] * a.w_post[e]) / rms1;
-    hs[e] = r;
-    a.hidden[e] = r;
-    if (a.hist_out) a.hist_out[e] = r;
-    s2 = fmaf(r, r, s2);
-  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+      const float r = res[i] + (v[i] * wq[i]) / rms1;
+      v[i] = r;
+      a.hidden[tid + 256 * i] = r;
+      if (a.hist_out) a.hist_out[tid + 256 * i] = r;
+      s2 = fmaf(r, r, s2);
+    }
   const float rms2 = sqrtf(block_sum256(s2, sh4) / (float)H + a.eps);
-  for (int e = tid; e < H; e += 256) a.normed[e] = (hs[e] * a.w_out[e]) / rms2;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) a.normed[tid + 256 * i] = (v[i] * wo[i]) / rms2;
   if (tid == 0) {
     a.st->pos += 1;
     a.st->cursor += 1;
@@ -430,14 +568,37 @@ __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
 
 // ---------------------------------------------------------------------------
 // Token selection over the logits (engine.ts:823-901).
-// Stage 1 (every block): per stride class c = i mod 256, the first index of
-// the class maximum over the block's stripes (strict >, init (-1e30, 0)), as
-// in argmax/topk256 (shaders.ts:337-347, 371-381).
-// Stage 2 (last block): merge stripes in order -> topk256; then either the
-// argmax halving tree (shaders.ts:351-357) or the host sampler
-// (engine.ts:862-901): repetition penalty in f64, stable descending sort,
-// f32-stored exp, f64 sums, top-p cutoff, walk with the injected draw u.
+// k_select1: per stride class c = i mod 256, the first index of the class
+// maximum over the block's stripes (strict >, init (-1e30, 0)), as in
+// argmax/topk256 (shaders.ts:337-347, 371-381).
+// k_select2: merge stripes in order -> topk256; then either the argmax
+// halving tree (shaders.ts:351-357) or the host sampler (engine.ts:862-901):
+// repetition penalty in f64, stable descending sort, f32-stored exp, f64
+// sums, top-p cutoff, walk with the injected draw u.
 // ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_select1(SelectArgs a) {
+  const int tid = threadIdx.x;
+  const int nb = gridDim.x;
+  const int stripes = (a.V + 255) / 256;
+  const int per = (stripes + nb - 1) / nb;
+  const int j0 = blockIdx.x * per, j1 = min(j0 + per, stripes);
+  float m = -1e30f;
+  uint32_t id = 0;
+  for (int j = j0; j < j1; j += 32) {
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const int i = (j + k) * 256 + tid;
+      v[k] = (j + k < j1 && i < a.V) ? a.logits[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (v[k] > m) { m = v[k]; id = (uint32_t)((j + k) * 256 + tid); }
+  }
+  a.cand_val[blockIdx.x * 256 + tid] = m;
+  a.cand_id[blockIdx.x * 256 + tid] = id;
+}
+
 struct Cand {
   double val;
   int ord;
@@ -448,46 +609,26 @@ __device__ __forceinline__ bool cand_before(const Cand& x, const Cand& y) {
   return x.val > y.val || (x.val == y.val && x.ord < y.ord);
 }
 
-__global__ __launch_bounds__(256) void k_select(SelectArgs a) {
+__global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
   __shared__ float tv[256];
   __shared__ uint32_t ti[256];
   __shared__ Cand cs[256];
   __shared__ float probs[256];
-  __shared__ int is_last;
   __shared__ int tok_sh;
   const int tid = threadIdx.x;
-  const int nb = gridDim.x;
-  const int stripes = (a.V + 255) / 256;
-  const int per = (stripes + nb - 1) / nb;
-  const int j0 = blockIdx.x * per, j1 = min(j0 + per, stripes);
   float m = -1e30f;
   uint32_t id = 0;
-  for (int j = j0; j < j1; ++j) {
-    const int i = j * 256 + tid;
-    if (i < a.V) {
-      const float v = a.logits[i];
-      if (v > m) { m = v; id = (uint32_t)i; }
+  for (int b0 = 0; b0 < nb; b0 += 32) {
+    float v[32];
+    uint32_t ix[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      v[k] = b0 + k < nb ? a.cand_val[(b0 + k) * 256 + tid] : -INFINITY;
+      ix[k] = b0 + k < nb ? a.cand_id[(b0 + k) * 256 + tid] : 0u;
     }
-  }
-  a.cand_val[blockIdx.x * 256 + tid] = m;
-  a.cand_id[blockIdx.x * 256 + tid] = id;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned int old =
-        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (old == (unsigned int)(nb - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-
-  // stage 2: class maxima in stripe order
-  m = -1e30f;
-  id = 0;
-  for (int bb = 0; bb < nb; ++bb) {
-    const float v = a.cand_val[bb * 256 + tid];
-    if (v > m) { m = v; id = a.cand_id[bb * 256 + tid]; }
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (v[k] > m) { m = v[k]; id = ix[k]; }
   }
   tv[tid] = m;
   ti[tid] = id;
@@ -512,8 +653,7 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a) {
     cd.val = (double)m;
     cd.ord = tid;
     cd.id = id;
-    if (rep > 1.0 && st->seen_count > 0 && id < (uint32_t)a.V &&
-        ((a.seen[id >> 5] >> (id & 31)) & 1u)) {
+    if (rep > 1.0 && st->seen_count > 0 && id < (uint32_t)a.V && ((a.seen[id >> 5] >> (id & 31)) & 1u)) {
       if (cd.val > 0) cd.val /= rep;
       else cd.val *= rep;
     }
@@ -562,34 +702,33 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a) {
   }
   if (tid == 0) {
     a.st->out_token = token;
-    if (a.out_token) *a.out_token = token;
     if (a.auto_add && token >= 0 && token < a.V) {
       a.seen[token >> 5] |= 1u << (token & 31);
       a.st->seen_count += 1;
     }
-    __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Upload helpers.
-// k_repack: GGUF row-major Q8_0 (rows of Kp 68-byte pairs) -> pair-interleaved.
-// interleave_half > 0 places source row r at fused row
-// (r / half) * 64 + (r % half) + dst_row_offset, i.e. gate rows in lanes 0..31
-// and (with dst_row_offset = 32) up rows in lanes 32..63 of each group.
+// k_repack: GGUF row-major Q8_0 (rows of Kp 68-byte pairs) -> the
+// pair-interleaved layout L. interleave_half > 0 places source row r at fused
+// row (r / half) * GR + (r % half) + dst_row_offset with half = GR / 2, i.e.
+// gate rows in the first half of each row group and (dst_row_offset = half)
+// the matching up rows in the second half.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_repack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                                long long rows, int Kp, long long off, int half) {
+                                                long long rows, Q8Layout L, long long off, int half) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long total = rows * Kp;
+  const long long total = rows * L.Kp;
   if (idx >= total) return;
-  const long long r = idx / Kp;
-  const int c = (int)(idx - r * Kp);
-  const long long R = half > 0 ? (r / half) * 64 + (r % half) + off : r + off;
-  const long long g = R >> 6;
-  const int ln = (int)(R & 63);
+  const long long r = idx / L.Kp;
+  const int c = (int)(idx - r * L.Kp);
+  const long long R = half > 0 ? (r / half) * L.GR + (r % half) + off : r + off;
+  const long long g = R / L.GR;
+  const int ln = (int)(R - g * L.GR);
   const uint32_t* s = (const uint32_t*)(src + (size_t)idx * kPairBytes);
-  uint32_t* d = (uint32_t*)(dst + (((size_t)g * Kp + c) * 64 + ln) * kPairBytes);
+  uint32_t* d = (uint32_t*)(dst + (((size_t)g * L.KpS + c / L.CI) * 64 + (c % L.CI) * L.GR + ln) * kPairBytes);
 #pragma unroll
   for (int i = 0; i < 17; ++i) d[i] = s[i];
 }
@@ -618,53 +757,80 @@ __global__ __launch_bounds__(256) void k_seen_add(uint32_t* seen, DevState* st, 
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-template <int PRO, int EPI>
+template <int PRO, int EPI, int CI, int NIF>
 static int launch_gemv_t(const GemvArgs& a, hipStream_t s) {
-  const size_t lds = (size_t)a.Kp * 64 * sizeof(float);
-  hipLaunchKernelGGL((k_gemv<PRO, EPI>), dim3(a.G * a.S), dim3(256), lds, s, a);
+  const size_t lds = (size_t)a.Kp * kXPad * sizeof(float);
+  hipLaunchKernelGGL((k_gemv<PRO, EPI, CI, NIF>), dim3(a.N / (64 / CI)), dim3(256), lds, s, a);
   return (int)hipGetLastError();
 }
 
-int launch_gemv(int pro, int epi, const GemvArgs& a, void* stream) {
-  hipStream_t s = (hipStream_t)stream;
-  if (a.Kp * 64 > kMaxK || a.Kp <= 0 || a.G <= 0 || a.S <= 0 || a.CS <= 0) return (int)hipErrorInvalidValue;
-  if (epi == EPI_GEGLU && a.S != 1) return (int)hipErrorInvalidValue;
-  if (pro == PRO_NONE && epi == EPI_PARTIAL) return launch_gemv_t<PRO_NONE, EPI_PARTIAL>(a, s);
-  if (pro == PRO_EMBED_NORM && epi == EPI_PARTIAL) return launch_gemv_t<PRO_EMBED_NORM, EPI_PARTIAL>(a, s);
-  if (pro == PRO_RESID_NORM && epi == EPI_PARTIAL) return launch_gemv_t<PRO_RESID_NORM, EPI_PARTIAL>(a, s);
-  if (pro == PRO_RESID_NORM && epi == EPI_GEGLU) return launch_gemv_t<PRO_RESID_NORM, EPI_GEGLU>(a, s);
+// Steps a wave issues before the prologue: all of them when a row group has
+// at most 4, 8 or 20 column steps; longer rows continue with a prefetch loop.
+template <int PRO, int EPI, int CI>
+static int launch_gemv_nif(const GemvArgs& a, hipStream_t s) {
+  if (a.KpS <= 4) return launch_gemv_t<PRO, EPI, CI, 1>(a, s);
+  if (a.KpS <= 8) return launch_gemv_t<PRO, EPI, CI, 2>(a, s);
+  return launch_gemv_t<PRO, EPI, CI, 5>(a, s);
+}
+
+template <int PRO, int EPI>
+static int launch_gemv_ci(int ci, const GemvArgs& a, hipStream_t s) {
+  switch (ci) {
+    case 1: return launch_gemv_nif<PRO, EPI, 1>(a, s);
+    case 8: return launch_gemv_nif<PRO, EPI, 8>(a, s);
+  }
   return (int)hipErrorInvalidValue;
 }
 
-int launch_sum_parts(const float* parts, int S, int N, float* y, void* stream) {
-  hipLaunchKernelGGL(k_sum_parts, dim3((N + 255) / 256), dim3(256), 0, (hipStream_t)stream, parts, S, N, y);
-  return (int)hipGetLastError();
+int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (a.Kp * 64 > kMaxK || a.Kp <= 0 || a.N <= 0 || (ci != 1 && ci != 8) || a.N % (64 / ci) ||
+      a.KpS != (a.Kp + ci - 1) / ci)
+    return (int)hipErrorInvalidValue;
+  if (pro != PRO_NONE && a.Kp * 64 > kMaxEPT / 4 * 256) return (int)hipErrorInvalidValue;
+  if (epi == EPI_GEGLU) {
+    if (pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
+    return launch_gemv_ci<PRO_RESID_NORM, EPI_GEGLU>(ci, a, s);
+  }
+  if (pro == PRO_NONE) return launch_gemv_ci<PRO_NONE, EPI_OUT>(ci, a, s);
+  if (pro == PRO_EMBED_NORM) return launch_gemv_ci<PRO_EMBED_NORM, EPI_OUT>(ci, a, s);
+  if (pro == PRO_RESID_NORM) return launch_gemv_ci<PRO_RESID_NORM, EPI_OUT>(ci, a, s);
+  return (int)hipErrorInvalidValue;
 }
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
   if (a.n_q < 1 || a.n_q > kMaxQHeads || grid < 1 || grid > kAttnMaxChunks) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  hipStream_t s = (hipStream_t)stream;
+  if (a.n_q <= 4) hipLaunchKernelGGL(k_attn<4>, dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(k_attn<8>, dim3(grid), dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(k_attn_combine, dim3(a.n_q * 4), dim3(64), 0, s, a);
   return (int)hipGetLastError();
 }
 
 int launch_final(const FinalArgs& a, void* stream) {
-  hipLaunchKernelGGL(k_final, dim3(1), dim3(256), (size_t)a.H * sizeof(float), (hipStream_t)stream, a);
+  if (a.H > 2048) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_final, dim3(1), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
 int launch_select(const SelectArgs& a, void* stream) {
   const int stripes = (a.V + 255) / 256;
   const int nb = stripes < kSelBlocks ? stripes : kSelBlocks;
-  hipLaunchKernelGGL(k_select, dim3(nb), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_select1, dim3(nb), dim3(256), 0, (hipStream_t)stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(k_select2, dim3(1), dim3(256), 0, (hipStream_t)stream, a, nb);
   return (int)hipGetLastError();
 }
 
-int launch_repack(const uint8_t* src, uint8_t* dst, long long rows, int Kp, long long off, int half,
+int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long rows, long long off, int half,
                   void* stream) {
-  const long long total = rows * Kp;
+  const long long total = rows * L.Kp;
   if (total <= 0) return 0;
   hipLaunchKernelGGL(k_repack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src,
-                     dst, rows, Kp, off, half);
+                     dst, rows, L, off, half);
   return (int)hipGetLastError();
 }
 

@@ -35,7 +35,7 @@ const char* kQ8Names[Q_NQ8] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn
 struct Layer {
   uint8_t* qkv = nullptr;   // fused [q | k | v] rows, pair-interleaved
   uint8_t* o = nullptr;
-  uint8_t* gu = nullptr;    // gate/up rows interleaved 32 + 32 per group
+  uint8_t* gu = nullptr;    // gate/up rows interleaved 32 + 32 per group (CI = 1)
   uint8_t* down = nullptr;
   float* norm[N_NNORM] = {};
   float* kc = nullptr;
@@ -83,21 +83,21 @@ struct gg_ctx {
   uint8_t* embd = nullptr;
   float* out_norm = nullptr;
   bool have_embd = false, have_out_norm = false;
+  Q8Layout lay_embd{}, lay_qkv{}, lay_o{}, lay_gu{}, lay_down{};
 
   // work buffers
-  float *qkv_part = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_part = nullptr;
-  float *act = nullptr, *down_part = nullptr, *hidden = nullptr, *residual = nullptr, *normed = nullptr;
+  float *qkv_out = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_out = nullptr;
+  float *act = nullptr, *down_out = nullptr, *hidden = nullptr, *residual = nullptr, *normed = nullptr;
   float *logits = nullptr, *hist = nullptr, *q_dbg = nullptr;
   float *freq_local = nullptr, *freq_global = nullptr;
   float* cand_val = nullptr;
   uint32_t *cand_id = nullptr, *top = nullptr, *seen = nullptr;
-  unsigned int* counters = nullptr;   // [0] attention, [1] selector
   DevState* st = nullptr;
   int32_t* tokens = nullptr;
   int32_t* d_ids = nullptr;           // staging for gg_penalty_add
   uint8_t* staging = nullptr;         // Q8_0 upload staging
   size_t staging_bytes = 0;
-  int S_qkv = 1, S_o = 1, S_down = 1, CS_qkv = 1, CS_o = 1, CS_down = 1, attn_grid = 1;
+  int attn_grid = 1;
 
   // pinned host mirrors
   DevState* h_st = nullptr;
@@ -110,6 +110,7 @@ struct gg_ctx {
   hipEvent_t probe_ev[2] = {nullptr, nullptr};
   bool probe_done = false;
   bool finalized = false, lost = false, timed = false;
+  bool use_graphs = true;   // GG_NO_GRAPH=1: launch the same kernels directly (profilers)
   std::vector<void*> allocs;
   std::string err;
 };
@@ -163,12 +164,6 @@ int launch_rc(gg_ctx* c, int rc, const char* what) {
 
 bool is_swa(const gg_config& c, int il) { return (il % c.swa_period) < (c.swa_period - 1); }
 
-// Column splits of a GEMV: cs pair-columns per block, S blocks per row group.
-void choose_split(int Kp, int cs_target, int* S, int* CS) {
-  int cs = cs_target < Kp ? cs_target : Kp;
-  *S = cdiv(Kp, cs);
-  *CS = cdiv(Kp, *S);
-}
 
 int check_ready(gg_ctx* c) {
   if (!c) return GG_ERR_INVALID;
@@ -189,14 +184,12 @@ struct ProbeScope {
   }
 };
 
-GemvArgs gemv_base(const uint8_t* W, int rows, int K, int S, int CS, float* out) {
+GemvArgs gemv_base(const uint8_t* W, const Q8Layout& L, float* out) {
   GemvArgs a{};
   a.W = W;
-  a.Kp = K / 64;
-  a.G = rows / 64;
-  a.S = S;
-  a.CS = CS;
-  a.N = rows;
+  a.Kp = L.Kp;
+  a.KpS = L.KpS;
+  a.N = L.rows;
   a.out = out;
   return a;
 }
@@ -207,7 +200,7 @@ int record_forward(gg_ctx* c) {
   for (int l = 0; l < c->L; ++l) {
     Layer& Ly = c->layers[l];
     // QKV with the previous layer's post-FFN norm + residual and attn_norm
-    GemvArgs q = gemv_base(Ly.qkv, c->NQKV, c->H, c->S_qkv, c->CS_qkv, c->qkv_part);
+    GemvArgs q = gemv_base(Ly.qkv, c->lay_qkv, c->qkv_out);
     q.w_pre = Ly.norm[N_ATTN];
     q.res_out = c->hidden;
     q.eps = eps;
@@ -217,22 +210,20 @@ int record_forward(gg_ctx* c) {
     ProbeScope ps(c, GG_PROBE_QKV, l);
     if (l == 0) {
       q.embd = c->embd;
-      q.Kp_embd = c->H / 64;
+      q.embd_KpS = c->lay_embd.KpS;
       q.embed_scale = sqrtf((float)c->H);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_EMBED_NORM, EPI_PARTIAL, q, c->stream), "qkv gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_EMBED_NORM, EPI_OUT, c->lay_qkv.CI, q, c->stream), "qkv gemv"));
     } else {
-      q.pre_part = c->down_part;
-      q.pre_S = c->S_down;
+      q.pre_vec = c->down_out;
       q.pre_res = c->residual;
       q.w_post = c->layers[l - 1].norm[N_POST_FFW];
       q.hist_out = c->hist + (size_t)(l - 1) * c->H;
-      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_PARTIAL, q, c->stream), "qkv gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_OUT, c->lay_qkv.CI, q, c->stream), "qkv gemv"));
     }
     }
     // attention
     AttnArgs at{};
-    at.qkv_part = c->qkv_part;
-    at.S = c->S_qkv;
+    at.qkv = c->qkv_out;
     at.n_q = c->NQ;
     at.q_norm = Ly.norm[N_QN];
     at.k_norm = Ly.norm[N_KN];
@@ -245,7 +236,6 @@ int record_forward(gg_ctx* c) {
     at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
     at.st = c->st;
     at.part = c->attn_part;
-    at.counter = c->counters;
     at.attn_out = c->attn_out;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
@@ -253,16 +243,15 @@ int record_forward(gg_ctx* c) {
       GG_TRY(launch_rc(c, launch_attention(at, c->attn_grid, c->stream), "attention"));
     }
     // O projection
-    GemvArgs o = gemv_base(Ly.o, c->H, c->QD, c->S_o, c->CS_o, c->o_part);
+    GemvArgs o = gemv_base(Ly.o, c->lay_o, c->o_out);
     o.x = c->attn_out;
     {
       ProbeScope ps(c, GG_PROBE_O, l);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, o, c->stream), "o gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_o.CI, o, c->stream), "o gemv"));
     }
     // gate/up with post-attn norm + residual + ffn_norm, GeGLU epilogue
-    GemvArgs gu = gemv_base(Ly.gu, 2 * c->I, c->H, 1, c->H / 64, nullptr);
-    gu.pre_part = c->o_part;
-    gu.pre_S = c->S_o;
+    GemvArgs gu = gemv_base(Ly.gu, c->lay_gu, nullptr);
+    gu.pre_vec = c->o_out;
     gu.pre_res = c->hidden;
     gu.w_post = Ly.norm[N_POST_ATTN];
     gu.w_pre = Ly.norm[N_FFN];
@@ -271,19 +260,18 @@ int record_forward(gg_ctx* c) {
     gu.act_out = c->act;
     {
       ProbeScope ps(c, GG_PROBE_GATE_UP, l);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_GEGLU, gu, c->stream), "gate/up gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_RESID_NORM, EPI_GEGLU, c->lay_gu.CI, gu, c->stream), "gate/up gemv"));
     }
     // down projection
-    GemvArgs d = gemv_base(Ly.down, c->H, c->I, c->S_down, c->CS_down, c->down_part);
+    GemvArgs d = gemv_base(Ly.down, c->lay_down, c->down_out);
     d.x = c->act;
     {
       ProbeScope ps(c, GG_PROBE_DOWN, l);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, d, c->stream), "down gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_down.CI, d, c->stream), "down gemv"));
     }
   }
   FinalArgs f{};
-  f.pre_part = c->down_part;
-  f.pre_S = c->S_down;
+  f.pre_vec = c->down_out;
   f.pre_res = c->residual;
   f.w_post = c->layers[c->L - 1].norm[N_POST_FFW];
   f.w_out = c->out_norm;
@@ -298,11 +286,11 @@ int record_forward(gg_ctx* c) {
 
 // Record LM head + selection (engine.ts:805-902).
 int record_select(gg_ctx* c) {
-  GemvArgs lm = gemv_base(c->embd, c->V, c->H, 1, c->H / 64, c->logits);
+  GemvArgs lm = gemv_base(c->embd, c->lay_embd, c->logits);
   lm.x = c->normed;
   {
     ProbeScope ps(c, GG_PROBE_LM_HEAD, -1);
-    GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_PARTIAL, lm, c->stream), "lm head"));
+    GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_embd.CI, lm, c->stream), "lm head"));
   }
   SelectArgs s{};
   s.logits = c->logits;
@@ -312,7 +300,6 @@ int record_select(gg_ctx* c) {
   s.top = c->top;
   s.seen = c->seen;
   s.st = c->st;
-  s.counter = c->counters + 1;
   s.auto_add = 1;
   ProbeScope ps(c, GG_PROBE_SELECT, -1);
   return launch_rc(c, launch_select(s, c->stream), "select");
@@ -331,6 +318,18 @@ int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
   e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
   if (e != hipSuccess) return hip_fail(c, e, "hipGraphInstantiate");
+  return GG_OK;
+}
+
+int run_forward(gg_ctx* c) {
+  if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
+  else GG_TRY(record_forward(c));
+  return GG_OK;
+}
+
+int run_select(gg_ctx* c) {
+  if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_sel, c->stream));
+  else GG_TRY(record_select(c));
   return GG_OK;
 }
 
@@ -356,13 +355,13 @@ gg_ctx* gg_create(const gg_config* cfg) {
   if (!cfg) { set_err(nullptr, GG_ERR_INVALID, "null config"); return nullptr; }
   const gg_config& k = *cfg;
   if (k.head_dim != kHeadDim || k.num_kv_heads != 1 || k.num_q_heads < 1 || k.num_q_heads > kMaxQHeads ||
-      k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > kMaxK || k.intermediate_size <= 0 ||
+      k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > 2048 || k.intermediate_size <= 0 ||
       k.intermediate_size % 64 || k.intermediate_size > kMaxK || k.vocab_size <= 0 || k.vocab_size % 64 ||
       k.num_layers <= 0 || k.context_length <= 0 || k.context_length > 32 * kAttnMaxChunks * 8 ||
       k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK) {
     set_err(nullptr, GG_ERR_INVALID,
             "unsupported config: needs head_dim 256, one KV head, <= 8 query heads, hidden/intermediate/vocab "
-            "multiples of 64 (<= 8192 for hidden/intermediate), context <= 65536");
+            "multiples of 64 (hidden <= 2048, intermediate <= 8192), context <= 65536");
     return nullptr;
   }
   int ndev = 0;
@@ -398,12 +397,18 @@ gg_ctx* gg_create(const gg_config* cfg) {
     c->err = "hipStreamCreate failed";
     return fail(0);
   }
-  // weights
-  auto q8bytes = [](long long rows, long long K) { return (size_t)(rows * K / 32 * 34); };
-  if (dalloc(c, &c->embd, q8bytes(c->V, c->H)) || dalloc(c, &c->out_norm, (size_t)c->H * 4)) return fail(0);
+  // weights: the tied embedding / LM head keeps whole 64-row groups (CI = 1,
+  // also what the embedding row lookup reads); every other matrix uses 8-row
+  // groups (CI = 8) so that a launch spreads over many blocks.
+  c->lay_embd = q8_layout(c->V, c->H, 1);
+  c->lay_qkv = q8_layout(c->NQKV, c->H, 8);
+  c->lay_o = q8_layout(c->H, c->QD, 8);
+  c->lay_gu = q8_layout(2 * c->I, c->H, 8);
+  c->lay_down = q8_layout(c->H, c->I, 8);
+  if (dalloc(c, &c->embd, c->lay_embd.bytes()) || dalloc(c, &c->out_norm, (size_t)c->H * 4)) return fail(0);
   for (Layer& Ly : c->layers) {
-    if (dalloc(c, &Ly.qkv, q8bytes(c->NQKV, c->H)) || dalloc(c, &Ly.o, q8bytes(c->H, c->QD)) ||
-        dalloc(c, &Ly.gu, q8bytes(2LL * c->I, c->H)) || dalloc(c, &Ly.down, q8bytes(c->H, c->I)))
+    if (dalloc(c, &Ly.qkv, c->lay_qkv.bytes()) || dalloc(c, &Ly.o, c->lay_o.bytes()) ||
+        dalloc(c, &Ly.gu, c->lay_gu.bytes()) || dalloc(c, &Ly.down, c->lay_down.bytes()))
       return fail(0);
     for (int j = 0; j < N_NNORM; ++j) {
       const int n = (j == N_QN || j == N_KN) ? kHeadDim : c->H;
@@ -468,22 +473,25 @@ int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t*
 
   // ---- Q8_0 matrices ----
   uint8_t* dst = nullptr;
+  const Q8Layout* lay = nullptr;
   long long rows = 0, K = 0, off = 0;
   int half = 0, bit = -1;
   if (layer < 0 && key == "token_embd") {
-    dst = c->embd; rows = c->V; K = c->H;
+    dst = c->embd; rows = c->V; K = c->H; lay = &c->lay_embd;
   } else if (layer >= 0) {
     Layer& Ly = c->layers[layer];
     for (int j = 0; j < Q_NQ8; ++j)
       if (key == kQ8Names[j]) bit = j;
     switch (bit) {
-      case Q_ATTN_Q: dst = Ly.qkv; rows = c->QD; K = c->H; off = 0; break;
-      case Q_ATTN_K: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD; break;
-      case Q_ATTN_V: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD + kHeadDim; break;
-      case Q_ATTN_O: dst = Ly.o; rows = c->H; K = c->QD; break;
-      case Q_GATE: dst = Ly.gu; rows = c->I; K = c->H; half = 32; off = 0; break;
-      case Q_UP: dst = Ly.gu; rows = c->I; K = c->H; half = 32; off = 32; break;
-      case Q_DOWN: dst = Ly.down; rows = c->H; K = c->I; break;
+      case Q_ATTN_Q: dst = Ly.qkv; rows = c->QD; K = c->H; off = 0; lay = &c->lay_qkv; break;
+      case Q_ATTN_K: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD; lay = &c->lay_qkv; break;
+      case Q_ATTN_V: dst = Ly.qkv; rows = kHeadDim; K = c->H; off = c->QD + kHeadDim; lay = &c->lay_qkv; break;
+      case Q_ATTN_O: dst = Ly.o; rows = c->H; K = c->QD; lay = &c->lay_o; break;
+      case Q_GATE: dst = Ly.gu; rows = c->I; K = c->H; half = c->lay_gu.GR / 2; off = 0; lay = &c->lay_gu; break;
+      case Q_UP:
+        dst = Ly.gu; rows = c->I; K = c->H; half = c->lay_gu.GR / 2; off = half; lay = &c->lay_gu;
+        break;
+      case Q_DOWN: dst = Ly.down; rows = c->H; K = c->I; lay = &c->lay_down; break;
       default: break;
     }
   }
@@ -501,7 +509,7 @@ int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t*
     c->staging_bytes = need;
   }
   GG_HIP(c, hipMemcpy(c->staging, bytes, need, hipMemcpyHostToDevice));
-  GG_TRY(launch_rc(c, launch_repack(c->staging, dst, rows, (int)(K / 64), off, half, c->stream), "repack"));
+  GG_TRY(launch_rc(c, launch_repack(c->staging, dst, *lay, rows, off, half, c->stream), "repack"));
   GG_TRY(sync(c, "repack"));
   if (layer < 0) c->have_embd = true;
   else c->layers[layer].have |= 1u << bit;
@@ -519,10 +527,7 @@ int gg_finalize(gg_ctx* c) {
       return set_err(c, GG_ERR_MISSING, "missing tensors of blk." + std::to_string(l));
   if (c->staging) { (void)hipFree(c->staging); c->staging = nullptr; c->staging_bytes = 0; }
 
-  choose_split(c->H / 64, 4, &c->S_qkv, &c->CS_qkv);
-  choose_split(c->QD / 64, 4, &c->S_o, &c->CS_o);
-  choose_split(c->I / 64, 8, &c->S_down, &c->CS_down);
-  c->attn_grid = std::min(kAttnMaxChunks, cdiv(c->CTX, 32));
+  c->attn_grid = std::min(kAttnMaxChunks, cdiv(c->CTX, kAttnChunk));
 
   const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
   for (Layer& Ly : c->layers) {
@@ -531,12 +536,12 @@ int gg_finalize(gg_ctx* c) {
     GG_HIP(c, hipMemset(Ly.kc, 0, kvb));
     GG_HIP(c, hipMemset(Ly.vc, 0, kvb));
   }
-  GG_TRY(dalloc(c, &c->qkv_part, (size_t)c->S_qkv * c->NQKV * 4));
+  GG_TRY(dalloc(c, &c->qkv_out, (size_t)c->NQKV * 4));
   GG_TRY(dalloc(c, &c->attn_part, (size_t)kAttnMaxChunks * c->NQ * (2 + kHeadDim) * 4));
   GG_TRY(dalloc(c, &c->attn_out, (size_t)c->QD * 4));
-  GG_TRY(dalloc(c, &c->o_part, (size_t)c->S_o * c->H * 4));
+  GG_TRY(dalloc(c, &c->o_out, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->act, (size_t)c->I * 4));
-  GG_TRY(dalloc(c, &c->down_part, (size_t)c->S_down * c->H * 4));
+  GG_TRY(dalloc(c, &c->down_out, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->hidden, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->residual, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->normed, (size_t)c->H * 4));
@@ -549,11 +554,9 @@ int gg_finalize(gg_ctx* c) {
   GG_TRY(dalloc(c, &c->cand_id, (size_t)kSelBlocks * 256 * 4));
   GG_TRY(dalloc(c, &c->top, 512 * 4));
   GG_TRY(dalloc(c, &c->seen, (size_t)cdiv(c->V, 32) * 4));
-  GG_TRY(dalloc(c, &c->counters, 64));
   GG_TRY(dalloc(c, &c->st, sizeof(DevState)));
   GG_TRY(dalloc(c, &c->tokens, (size_t)c->CTX * 4));
   GG_TRY(dalloc(c, &c->d_ids, (size_t)c->CTX * 4));
-  GG_HIP(c, hipMemset(c->counters, 0, 64));
   GG_HIP(c, hipMemset(c->st, 0, sizeof(DevState)));
   GG_HIP(c, hipMemset(c->seen, 0, (size_t)cdiv(c->V, 32) * 4));
   GG_HIP(c, hipMemset(c->tokens, 0, (size_t)c->CTX * 4));
@@ -581,8 +584,12 @@ int gg_finalize(gg_ctx* c) {
   if (c->probe_kind != GG_PROBE_NONE)
     for (int i = 0; i < 2; ++i) GG_HIP(c, hipEventCreate(&c->probe_ev[i]));
 
-  GG_TRY(capture(c, record_forward, &c->g_fwd));
-  GG_TRY(capture(c, record_select, &c->g_sel));
+  const char* ng = getenv("GG_NO_GRAPH");
+  c->use_graphs = !(ng && ng[0] == '1');
+  if (c->use_graphs) {
+    GG_TRY(capture(c, record_forward, &c->g_fwd));
+    GG_TRY(capture(c, record_select, &c->g_sel));
+  }
   c->finalized = true;
   return GG_OK;
 }
@@ -600,7 +607,7 @@ int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
   c->h_st->cursor = 0;
   GG_HIP(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
   GG_TRY(push_state(c, 0, offsetof(DevState, temperature)));
-  for (int i = 0; i < n; ++i) GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
+  for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
   c->timed = false;
   return sync(c, "prefill");
 }
@@ -613,13 +620,13 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (with_forward) {
     GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
     GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
-    GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
+    GG_TRY(run_forward(c));
   } else {
     GG_TRY(push_state(c, offsetof(DevState, temperature), offsetof(DevState, seen_count)));
     GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
   }
   GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
-  GG_HIP(c, hipGraphLaunch(c->g_sel, c->stream));
+  GG_TRY(run_select(c));
   GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
   GG_HIP(c, hipMemcpyAsync(c->h_out, (char*)c->st + offsetof(DevState, out_token), 4, hipMemcpyDeviceToHost,
                            c->stream));
@@ -756,27 +763,23 @@ void gg_destroy(gg_ctx* c) {
 
 // ---- kernel-level entry points --------------------------------------------
 
-int gg_q8_0_repack(const void* src, void* dst, int64_t rows, int64_t k, void* stream) {
-  if (!src || !dst || rows <= 0 || k <= 0 || rows % 64 || k % 64 || k / 64 > (1 << 30)) return GG_ERR_INVALID;
-  const int rc = launch_repack((const uint8_t*)src, (uint8_t*)dst, rows, (int)(k / 64), 0, 0, stream);
-  return rc ? GG_ERR_HIP : GG_OK;
+size_t gg_q8_0_packed_size(int64_t rows, int64_t k) {
+  if (rows <= 0 || k <= 0 || rows % 64 || k % 64 || rows > (1LL << 30) || k > kMaxK) return 0;
+  return q8_layout((int)rows, (int)k).bytes();
 }
 
-int gg_q8_0_gemv(const void* w, const float* x, float* y, int64_t rows, int64_t k, int32_t splits,
-                 float* workspace, void* stream) {
-  if (!w || !x || !y || rows <= 0 || k <= 0 || rows % 64 || k % 64 || k > kMaxK || rows / 64 > (1 << 24))
-    return GG_ERR_INVALID;
-  const int Kp = (int)(k / 64);
-  int S = 1, CS = Kp;
-  if (splits > 1) {
-    if (!workspace) return GG_ERR_INVALID;
-    choose_split(Kp, cdiv(Kp, splits), &S, &CS);
-  }
-  GemvArgs a = gemv_base((const uint8_t*)w, (int)rows, (int)k, S, CS, S > 1 ? workspace : y);
+int gg_q8_0_repack(const void* src, void* dst, int64_t rows, int64_t k, void* stream) {
+  if (!src || !dst || !gg_q8_0_packed_size(rows, k)) return GG_ERR_INVALID;
+  const Q8Layout L = q8_layout((int)rows, (int)k);
+  return launch_repack((const uint8_t*)src, (uint8_t*)dst, L, rows, 0, 0, stream) ? GG_ERR_HIP : GG_OK;
+}
+
+int gg_q8_0_gemv(const void* w, const float* x, float* y, int64_t rows, int64_t k, void* stream) {
+  if (!w || !x || !y || !gg_q8_0_packed_size(rows, k)) return GG_ERR_INVALID;
+  const Q8Layout L = q8_layout((int)rows, (int)k);
+  GemvArgs a = gemv_base((const uint8_t*)w, L, y);
   a.x = x;
-  if (launch_gemv(PRO_NONE, EPI_PARTIAL, a, stream)) return GG_ERR_HIP;
-  if (S > 1 && launch_sum_parts(workspace, S, (int)rows, y, stream)) return GG_ERR_HIP;
-  return GG_OK;
+  return launch_gemv(PRO_NONE, EPI_OUT, L.CI, a, stream) ? GG_ERR_HIP : GG_OK;
 }
 
 int gg_q8_0_dequant(const void* src, float* out, int64_t n, void* stream) {
@@ -784,10 +787,10 @@ int gg_q8_0_dequant(const void* src, float* out, int64_t n, void* stream) {
   return launch_dequant((const uint8_t*)src, out, n, stream) ? GG_ERR_HIP : GG_OK;
 }
 
-// workspace: DevState | counter | cand_val | cand_id | top | out
+// workspace: DevState | cand_val | cand_id | top
 size_t gg_select_workspace_size(int32_t n) {
   (void)n;
-  return 256 + 64 + (size_t)kSelBlocks * 256 * 8 + 512 * 4 + 64;
+  return 256 + (size_t)kSelBlocks * 256 * 8 + 512 * 4;
 }
 
 int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s, double u,
@@ -805,15 +808,12 @@ int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const
   a.logits = logits;
   a.V = n;
   a.st = (DevState*)ws;
-  a.counter = (unsigned int*)(ws + 256);
-  a.cand_val = (float*)(ws + 320);
-  a.cand_id = (uint32_t*)(ws + 320 + (size_t)kSelBlocks * 256 * 4);
-  a.top = topk_out ? (uint32_t*)topk_out : (uint32_t*)(ws + 320 + (size_t)kSelBlocks * 256 * 8);
+  a.cand_val = (float*)(ws + 256);
+  a.cand_id = (uint32_t*)(ws + 256 + (size_t)kSelBlocks * 256 * 4);
+  a.top = topk_out ? (uint32_t*)topk_out : (uint32_t*)(ws + 256 + (size_t)kSelBlocks * 256 * 8);
   a.seen = seen ? (uint32_t*)seen : (uint32_t*)ws;  // never read when seen_count == 0
-  a.out_token = nullptr;
   a.auto_add = 0;
   if (hipMemcpyAsync(ws, &h, sizeof(h), hipMemcpyHostToDevice, hs) != hipSuccess) return GG_ERR_HIP;
-  if (hipMemsetAsync(a.counter, 0, 4, hs) != hipSuccess) return GG_ERR_HIP;
   if (launch_select(a, hs)) return GG_ERR_HIP;
   DevState back{};
   if (hipMemcpyAsync(&back, ws, sizeof(back), hipMemcpyDeviceToHost, hs) != hipSuccess) return GG_ERR_HIP;

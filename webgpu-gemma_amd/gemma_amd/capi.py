@@ -96,8 +96,9 @@ _SIGS = {
     "gg_probe_elapsed": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
     "gg_last_error": (ctypes.c_char_p, [_P]),
     "gg_destroy": (None, [_P]),
+    "gg_q8_0_packed_size": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "gg_q8_0_repack": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P]),
-    "gg_q8_0_gemv": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _P, _P]),
+    "gg_q8_0_gemv": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, ctypes.c_int64, _P]),
     "gg_q8_0_dequant": (ctypes.c_int, [_P, _P, ctypes.c_int64, _P]),
     "gg_select_workspace_size": (ctypes.c_size_t, [ctypes.c_int32]),
     "gg_select_logits": (ctypes.c_int, [_P, ctypes.c_int32, _P, ctypes.POINTER(GGSample), ctypes.c_double, _P, _P,
@@ -244,9 +245,12 @@ def q8_0_repack(src_ptr: int, dst_ptr: int, rows: int, k: int, stream=None):
     _check(None, lib().gg_q8_0_repack(src_ptr, dst_ptr, rows, k, _stream_ptr(stream)))
 
 
-def q8_0_gemv(w_ptr: int, x_ptr: int, y_ptr: int, rows: int, k: int, splits: int = 1, ws_ptr: int = 0,
-              stream=None):
-    _check(None, lib().gg_q8_0_gemv(w_ptr, x_ptr, y_ptr, rows, k, splits, ws_ptr or None, _stream_ptr(stream)))
+def q8_0_packed_size(rows: int, k: int) -> int:
+    return int(lib().gg_q8_0_packed_size(rows, k))
+
+
+def q8_0_gemv(w_ptr: int, x_ptr: int, y_ptr: int, rows: int, k: int, stream=None):
+    _check(None, lib().gg_q8_0_gemv(w_ptr, x_ptr, y_ptr, rows, k, _stream_ptr(stream)))
 
 
 def q8_0_dequant(src_ptr: int, out_ptr: int, n: int, stream=None):
