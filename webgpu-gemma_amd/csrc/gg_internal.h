@@ -23,12 +23,12 @@
 namespace gg {
 
 constexpr int kHeadDim = 256;        // Gemma-3 270M/1B head_dim
-constexpr int kMaxQHeads = 8;
+constexpr int kAttnMaxQ = 4;         // query heads per KV head the attention kernel takes
 constexpr int kPairBytes = 68;
 constexpr int kColBytes = 64 * kPairBytes;   // one wavefront step: 4352 bytes
 constexpr int kMaxK = 8192;          // largest GEMV input (x staged in LDS)
 constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
-constexpr int kAttnChunk = 64;       // base positions per attention block
+constexpr int kAttnChunk = 32;       // base positions per attention block (4 waves x 8)
 constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per token
 
 // Q8_0 matrix in the pair-interleaved layout.
@@ -95,7 +95,7 @@ struct AttnArgs {
   int n_q;                 // query heads (one KV head)
   const float* q_norm;     // [256]
   const float* k_norm;     // [256]
-  const float* freq;       // [128] RoPE inverse frequencies for this layer
+  const float* rope;       // [ctx][2][128] cos / sin of f32(pos) * freq[i], this layer's theta
   float* k_cache;          // [ctx][256]
   float* v_cache;          // [ctx][256]
   int window;              // 0: full causal attention
@@ -103,7 +103,8 @@ struct AttnArgs {
   float scale;             // 1/sqrt(head_dim)
   const DevState* st;
   float* part;             // [kAttnMaxChunks][n_q][2 + 256]
-  float* attn_out;         // [n_q * 256] (combine kernel)
+  unsigned int* counter;   // arrivals of the chunk blocks (reset by the last)
+  float* attn_out;         // [n_q * 256]
   float* q_dbg;            // optional: normed+roped q of this token
 };
 

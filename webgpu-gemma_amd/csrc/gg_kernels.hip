@@ -1,12 +1,11 @@
 // gg_kernels.hip -- gfx950 (CDNA4) kernels of the Gemma-3 Q8_0 token loop.
 //
-// One forward pass over a token is six kernels per layer:
+// One forward pass over a token is five kernels per layer:
 //   k_gemv<EMBED_NORM|RESID_NORM, OUT>  fused QKV projection; its prologue
 //        finishes the previous layer (post-FFN norm + residual) and applies
 //        attn_norm (engine.ts:768-774, 794)
 //   k_attn          QK-norm + RoPE + KV store + one chunk of decode attention
-//                   per block (engine.ts:775-783)
-//   k_attn_combine  merge of the chunk softmax statistics
+//                   per block; the last block merges the chunks (engine.ts:775-783)
 //   k_gemv<NONE, OUT>          attention output projection (engine.ts:784)
 //   k_gemv<RESID_NORM, GEGLU>  post-attn norm + residual + ffn_norm, gate and
 //                   up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
@@ -15,9 +14,10 @@
 // and for a sampled step the LM head GEMV plus k_select1/k_select2
 // (engine.ts:817-901).
 //
-// No kernel communicates between its blocks: on this multi-XCD part a
-// device-scope fence is an L2 write-back, so every cross-block dependency is
-// a kernel boundary of the captured graph instead.
+// On this multi-XCD part a device-scope fence is a whole-L2 write-back, so
+// kernels never fence. The one in-kernel cross-block step (the attention
+// chunk merge) exchanges data with write-through device-scope stores/loads
+// and a device-scope counter; everything else is a graph kernel boundary.
 //
 // All arithmetic is fp32 except the int8 weight payload (dequantised exactly
 // in registers) and the sampler's f64 steps, which mirror the JS host's.
@@ -32,7 +32,6 @@ namespace gg {
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kXPad = 68;          // LDS floats per 64-wide x segment (4 pad: no bank conflicts)
-constexpr int kAttnMaxCh = 256;    // largest attention chunk (positions per block)
 
 // ---------------------------------------------------------------------------
 // helpers
@@ -66,6 +65,14 @@ __device__ __forceinline__ float block_sum256(float v, float* sh4) {
   if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
   __syncthreads();
   return ((sh4[0] + sh4[1]) + sh4[2]) + sh4[3];
+}
+
+__device__ __forceinline__ float block_max256(float v, float* sh4) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(sh4[0], sh4[1]), fmaxf(sh4[2], sh4[3]));
 }
 
 // One 68-byte pair = blocks 2c and 2c+1 of a row: 17 dwords.
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // (fusedPerHeadNormRope, shaders.ts:420-467); the block holding `pos` stores
 // k/v into the cache (kvCacheStore, shaders.ts:209-227) and reads them from
 // LDS. Scores/softmax/weighted-V follow shaders.ts:229-325 within the chunk
-// and leave (max, sum, o) per head for k_attn_combine.
+// and leave (max, sum, o) per head; the last block to finish merges them.
 //
 // Scores: wave w takes P = 64/NQP positions at a time with one float4 of the
 // head per lane; the P*NQP = 64 partial dots per lane are finished by one
@@ -288,15 +295,32 @@ __device__ __forceinline__ void attn_span(const AttnArgs& a, int pos, int* t_lo,
   *nch = (span + c - 1) / c;
 }
 
-template <int NQP>
+// Device-scope (write-through / L2-bypassing) accesses for the chunk
+// statistics that the last block of k_attn merges; unlike a device-scope
+// fence they do not write back the whole L2.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lane l of a wave works on position p = l / 8 of the wave's pass and on
+// dims [32 o, 32 o + 32) with o = l % 8 for the scores, and on dims
+// [4 l, 4 l + 4) of every position for the weighted sum of V.
+constexpr int kAttnP = 8;   // positions per wave pass
+constexpr int kQPad = 288;  // LDS floats per head: 8 octants of 32 dims + 4 pad each
+__device__ __forceinline__ int qidx(int d) { return (d >> 5) * 36 + (d & 31); }
+
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
-  constexpr int P = 64 / NQP;
-  __shared__ float qs[NQP][kHeadDim];
-  __shared__ float ks[kHeadDim];
+  constexpr int NQ = kAttnMaxQ;
+  __shared__ float qs[NQ][kQPad];
+  __shared__ float ks[kQPad];
   __shared__ float vs[kHeadDim];
-  __shared__ float pw[4][64];
-  __shared__ float wm[4][NQP], wl[4][NQP];
-  __shared__ float wo[4][NQP][kHeadDim];
+  __shared__ float pw[4][kAttnP * NQ];
+  __shared__ float wm[4][NQ], wl[4][NQ];
+  __shared__ float wo[4][NQ][kHeadDim];
+  __shared__ float sm[kAttnMaxChunks * NQ];
+  __shared__ float sf[kAttnMaxChunks * NQ];
+  __shared__ float hstat[NQ][2];
+  __shared__ int is_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
@@ -307,220 +331,300 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   if (b >= nch) return;
   const int t0 = t_lo + b * ch;
   const int t1 = min(t0 + ch, pos + 1);
-
-  // 1. q, k, v from the QKV output (query heads beyond n_q are zero)
   const int nqd = nq * kHeadDim;
-  for (int e = tid; e < NQP * kHeadDim; e += 256) qs[e >> 8][e & 255] = e < nqd ? a.qkv[e] : 0.f;
-  ks[tid] = a.qkv[nqd + tid];
-  vs[tid] = a.qkv[nqd + kHeadDim + tid];
-  __syncthreads();
+  const int pl = lane >> 3, oc = lane & 7;
 
-  // 2. per-head RMSNorm (q heads, then the k head)
-  for (int h = wv; h <= nq; h += 4) {
-    float* hp = (h < nq) ? qs[h] : ks;
-    const float* w = (h < nq) ? a.q_norm : a.k_norm;
-    float x[4];
+  // 0. loads that do not depend on q: this wave's first pass of K rows (lane
+  // layout of the scores) and V rows (lane layout of the weighted sum), the
+  // QKV output, the norm weights and the RoPE frequencies
+  const int tb0 = t0 + wv * kAttnP;
+  float4 kr[8], vr[kAttnP];
+  {
+    const int t = tb0 + pl;
+    if (t < pos && t < t1) {
+      const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kr[j] = kp[j];
+    }
+#pragma unroll
+    for (int i = 0; i < kAttnP; ++i) {
+      const int tv = tb0 + i;
+      if (tv < pos && tv < t1) vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
+    }
+  }
+  const bool my_head = wv < nq;
+  const bool k_head = (wv == 0) && (b == nch - 1);
+  float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hx[i] = my_head ? a.qkv[wv * kHeadDim + lane + 64 * i] : 0.f;
+    nwt[i] = a.q_norm[lane + 64 * i];
+    kx[i] = a.qkv[nqd + lane + 64 * i];
+    kwt[i] = a.k_norm[lane + 64 * i];
+  }
+  // RoPE table row of this position: cos(f32(pos) * freq[i]), sin(...)
+  const float* rt = a.rope + (size_t)pos * 2 * (kHeadDim / 2);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cs[j] = rt[lane + 64 * j];
+    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
+  }
+  if (tid < kHeadDim) vs[tid] = a.qkv[nqd + kHeadDim + tid];
+
+  // 1. wave w: RMSNorm + NEOX RoPE of query head w (and, in the block that
+  // holds `pos`, wave 0 also of the key head) -- fusedPerHeadNormRope,
+  // shaders.ts:420-467. Lane owns dims lane + 64 i; pairs (i, i + 128).
+  auto norm_rope = [&](float* x, const float* w, float* dst) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { x[i] = hp[lane + 64 * i]; ss = fmaf(x[i], x[i], ss); }
+    for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
     ss = wave_sum(ss);
     const float rms = sqrtf(ss / (float)kHeadDim + a.eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hp[lane + 64 * i] = (x[i] * w[lane + 64 * i]) / rms;
+    for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) / rms;
+    // dims lane, lane+64 pair with lane+128, lane+192
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float x0 = x[j], x1 = x[j + 2];
+      dst[qidx(lane + 64 * j)] = x0 * cs[j] - x1 * sn[j];
+      dst[qidx(lane + 64 * j + 128)] = x0 * sn[j] + x1 * cs[j];
+    }
+  };
+  if (my_head) norm_rope(hx, nwt, qs[wv]);
+  else if (wv < NQ) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs[wv][qidx(lane + 64 * i)] = 0.f;
   }
-  __syncthreads();
-
-  // 3. NEOX RoPE on pairs (i, i+128): angle = f32(pos) * freq[i]
-  for (int idx = tid; idx < (nq + 1) * (kHeadDim / 2); idx += 256) {
-    const int h = idx >> 7, i = idx & 127;
-    float* hp = (h < nq) ? qs[h] : ks;
-    const float angle = (float)pos * a.freq[i];
-    float sn, cs;
-    sincosf(angle, &sn, &cs);
-    const float x0 = hp[i], x1 = hp[i + 128];
-    hp[i] = x0 * cs - x1 * sn;
-    hp[i + 128] = x0 * sn + x1 * cs;
-  }
+  if (k_head) norm_rope(kx, kwt, ks);
   __syncthreads();
 
   if (b == nch - 1) {
-    a.k_cache[(size_t)pos * kHeadDim + tid] = ks[tid];
+    a.k_cache[(size_t)pos * kHeadDim + tid] = ks[qidx(tid)];
     a.v_cache[(size_t)pos * kHeadDim + tid] = vs[tid];
   }
   if (b == 0 && a.q_dbg)
-    for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = qs[e >> 8][e & 255];
+    for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = qs[e >> 8][qidx(e & 255)];
 
-  // 4. per-wave online softmax over passes of P positions; lane holds 4 dims
-  float4 q4[NQP];
+  // q slice of this lane's score layout: 4 heads x 32 dims in registers
+  float4 qr[NQ][8];
 #pragma unroll
-  for (int h = 0; h < NQP; ++h) q4[h] = *(const float4*)&qs[h][4 * lane];
-  float m[NQP], l[NQP];
-  float4 o4[NQP];
+  for (int h = 0; h < NQ; ++h)
 #pragma unroll
-  for (int h = 0; h < NQP; ++h) {
+    for (int j = 0; j < 8; ++j) qr[h][j] = *(const float4*)&qs[h][36 * oc + 4 * j];
+
+  // 2. per-wave online softmax over passes of kAttnP positions
+  float m[NQ], l[NQ];
+  float4 o4[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.f;
     o4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const int my_h = lane % NQP;
-  for (int tb = t0 + wv * P; tb < t1; tb += 4 * P) {
-    float4 kr[P], vr[P];
+  for (int tb = tb0; tb < t1; tb += 4 * kAttnP) {
+    const int t = tb + pl;
+    if (tb != tb0 && t < pos && t < t1) {
+      const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const int t = tb + i;
-      if (t < pos) {
-        kr[i] = *(const float4*)(a.k_cache + (size_t)t * kHeadDim + 4 * lane);
-        vr[i] = *(const float4*)(a.v_cache + (size_t)t * kHeadDim + 4 * lane);
-      } else if (t == pos) {
-        kr[i] = *(const float4*)&ks[4 * lane];
-        vr[i] = *(const float4*)&vs[4 * lane];
-      } else {
-        kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[i] = kr[i];
-      }
+      for (int j = 0; j < 8; ++j) kr[j] = kp[j];
     }
-    float v[64];
+    if (t == pos) {
 #pragma unroll
-    for (int i = 0; i < P; ++i)
-#pragma unroll
-      for (int h = 0; h < NQP; ++h) {
-        float d = q4[h].x * kr[i].x;
-        d = fmaf(q4[h].y, kr[i].y, d);
-        d = fmaf(q4[h].z, kr[i].z, d);
-        d = fmaf(q4[h].w, kr[i].w, d);
-        v[i * NQP + h] = d;
-      }
-    // reduce-scatter: afterwards lane l owns the full dot of index l
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const bool hi = (lane & msk) != 0;
-#pragma unroll
-      for (int i = 0; i < msk; ++i) {
-        const float send = hi ? v[i] : v[i + msk];
-        const float keep = hi ? v[i + msk] : v[i];
-        v[i] = keep + __shfl_xor(send, msk, 64);
-      }
+      for (int j = 0; j < 8; ++j) kr[j] = *(const float4*)&ks[36 * oc + 4 * j];
     }
-    const bool valid = tb + lane / NQP < t1 && my_h < nq;
-    const float sco = valid ? v[0] * a.scale : -INFINITY;
-    // pass maximum of head my_h over the lanes holding that head
-    float mx = sco;
 #pragma unroll
-    for (int msk = NQP; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-    float alpha[NQP], m_own = -INFINITY;
+    for (int i = 0; i < kAttnP; ++i) {
+      const int tv = tb + i;
+      if (tv == pos) vr[i] = *(const float4*)&vs[4 * lane];
+      else if (tb != tb0 && tv < pos && tv < t1)
+        vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
+    }
+    const bool valid = t < t1;
+    float sc[NQ];
 #pragma unroll
-    for (int h = 0; h < NQP; ++h) {
-      const float mn = fmaxf(m[h], __shfl(mx, h, 64));
+    for (int h = 0; h < NQ; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d = fmaf(qr[h][j].x, kr[j].x, d);
+        d = fmaf(qr[h][j].y, kr[j].y, d);
+        d = fmaf(qr[h][j].z, kr[j].z, d);
+        d = fmaf(qr[h][j].w, kr[j].w, d);
+      }
+      d += __shfl_xor(d, 1, 64);
+      d += __shfl_xor(d, 2, 64);
+      d += __shfl_xor(d, 4, 64);
+      sc[h] = (valid && h < nq) ? d * a.scale : -INFINITY;
+    }
+    float alpha[NQ], p[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      float mx = sc[h];
+      mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m[h], mx);
       alpha[h] = (m[h] == -INFINITY) ? 0.f : expf(m[h] - mn);
+      p[h] = (sc[h] == -INFINITY) ? 0.f : expf(sc[h] - mn);
+      float ps = p[h];
+      ps += __shfl_xor(ps, 8, 64);
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      l[h] = fmaf(l[h], alpha[h], ps);
       m[h] = mn;
-      if (h == my_h) m_own = mn;
     }
-    const float p = valid ? expf(sco - m_own) : 0.f;
-    float ps = p;
+    if (oc == 0) {
 #pragma unroll
-    for (int msk = NQP; msk < 64; msk <<= 1) ps += __shfl_xor(ps, msk, 64);
-    pw[wv][lane] = p;
+      for (int h = 0; h < NQ; ++h) pw[wv][pl * NQ + h] = p[h];
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int h = 0; h < NQP; ++h) {
-      l[h] = fmaf(l[h], alpha[h], __shfl(ps, h, 64));
+    for (int h = 0; h < NQ; ++h) {
       o4[h].x *= alpha[h];
       o4[h].y *= alpha[h];
       o4[h].z *= alpha[h];
       o4[h].w *= alpha[h];
     }
 #pragma unroll
-    for (int i = 0; i < P; ++i)
+    for (int i = 0; i < kAttnP; ++i) {
+      const float4 pp = *(const float4*)&pw[wv][i * NQ];
+      const float pv[4] = {pp.x, pp.y, pp.z, pp.w};
+      if (tb + i < t1) {
 #pragma unroll
-      for (int h = 0; h < NQP; ++h) {
-        const float pp = pw[wv][i * NQP + h];
-        o4[h].x = fmaf(pp, vr[i].x, o4[h].x);
-        o4[h].y = fmaf(pp, vr[i].y, o4[h].y);
-        o4[h].z = fmaf(pp, vr[i].z, o4[h].z);
-        o4[h].w = fmaf(pp, vr[i].w, o4[h].w);
+        for (int h = 0; h < NQ; ++h) {
+          o4[h].x = fmaf(pv[h], vr[i].x, o4[h].x);
+          o4[h].y = fmaf(pv[h], vr[i].y, o4[h].y);
+          o4[h].z = fmaf(pv[h], vr[i].z, o4[h].z);
+          o4[h].w = fmaf(pv[h], vr[i].w, o4[h].w);
+        }
       }
+    }
     __builtin_amdgcn_wave_barrier();
   }
 
-  // 5. merge the four waves (fixed order) into this chunk's (max, sum, o)
-  if (lane < NQP) {
+  // 3. merge the four waves (fixed order) into this chunk's (max, sum, o)
+  if (lane < NQ) {
     float mm = m[0], ll = l[0];
 #pragma unroll
-    for (int h = 1; h < NQP; ++h)
+    for (int h = 1; h < NQ; ++h)
       if (lane == h) { mm = m[h]; ll = l[h]; }
     wm[wv][lane] = mm;
     wl[wv][lane] = ll;
   }
 #pragma unroll
-  for (int h = 0; h < NQP; ++h) *(float4*)&wo[wv][h][4 * lane] = o4[h];
+  for (int h = 0; h < NQ; ++h) *(float4*)&wo[wv][h][4 * lane] = o4[h];
   __syncthreads();
   const size_t pstride = (size_t)nq * (2 + kHeadDim);
-  float* mypart = a.part + (size_t)b * pstride;
-  for (int h = 0; h < nq; ++h) {
-    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-    float L = 0.f, O = 0.f;
+  float O[NQ];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
-      L = fmaf(f, wl[w][h], L);
-      O = fmaf(f, wo[w][h][tid], O);
-    }
-    mypart[h * (2 + kHeadDim) + 2 + tid] = O;
-    if (tid == 0) {
-      mypart[h * (2 + kHeadDim)] = M;
-      mypart[h * (2 + kHeadDim) + 1] = L;
-    }
-  }
-}
-
-// Merge the chunk statistics: block = (head, quarter of the head dims).
-// Loads of all chunk statistics and outputs are issued before any arithmetic.
-__global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a) {
-  __shared__ float fac[kAttnMaxChunks];
-  const int lane = threadIdx.x;
-  const int h = blockIdx.x >> 2, d = (blockIdx.x & 3) * 64 + lane;
-  const int pos = a.st->pos;
-  int t_lo, ch, nch;
-  attn_span(a, pos, &t_lo, &ch, &nch);
-  const size_t pstride = (size_t)a.n_q * (2 + kHeadDim);
-  const float* ph = a.part + h * (2 + kHeadDim);
-  float mc[kAttnMaxChunks / 64], lc[kAttnMaxChunks / 64];
+  for (int h = 0; h < NQ; ++h) {
+    O[h] = 0.f;
+    if (h < nq) {
+      const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+      float L = 0.f, Ov = 0.f;
 #pragma unroll
-  for (int i = 0; i < kAttnMaxChunks / 64; ++i) {
-    const int c = lane + 64 * i;
-    mc[i] = c < nch ? ph[c * pstride] : -INFINITY;
-    lc[i] = c < nch ? ph[c * pstride + 1] : 0.f;
-  }
-  float o = 0.f, L = 0.f;
-  for (int c0 = 0; c0 < nch; c0 += 32) {
-    float ov[32];
-#pragma unroll
-    for (int k = 0; k < 32; ++k) ov[k] = c0 + k < nch ? ph[(c0 + k) * pstride + 2 + d] : 0.f;
-    if (c0 == 0) {
-      float m = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < kAttnMaxChunks / 64; ++i) m = fmaxf(m, mc[i]);
-      const float M = wave_max(m);
-      float l = 0.f;
-#pragma unroll
-      for (int i = 0; i < kAttnMaxChunks / 64; ++i) {
-        const int c = lane + 64 * i;
-        if (c < nch) {
-          const float f = expf(mc[i] - M);
-          fac[c] = f;
-          l = fmaf(f, lc[i], l);
-        }
+      for (int w = 0; w < 4; ++w) {
+        const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
+        L = fmaf(f, wl[w][h], L);
+        Ov = fmaf(f, wo[w][h][tid], Ov);
       }
-      L = wave_sum(l);
-      __syncthreads();
+      O[h] = Ov;
+      if (tid == 0) { hstat[h][0] = M; hstat[h][1] = L; }
+    }
+  }
+  if (nch == 1) {   // a single chunk is the result
+    __syncthreads();
+    for (int h = 0; h < nq; ++h) a.attn_out[h * kHeadDim + tid] = O[h] / hstat[h][1];
+    return;
+  }
+  float* mypart = a.part + (size_t)b * pstride;
+  for (int h = 0; h < nq; ++h) st_dev(mypart + h * (2 + kHeadDim) + 2 + tid, O[h]);
+  __syncthreads();
+  if (tid < nq) {
+    st_dev(mypart + tid * (2 + kHeadDim), hstat[tid][0]);
+    st_dev(mypart + tid * (2 + kHeadDim) + 1, hstat[tid][1]);
+  }
+
+  // 4. the last block to finish merges every chunk. Partials are written
+  // through to the device coherence point and the counter is a device-scope
+  // atomic issued after all of this block's stores have completed.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int old = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = (old == (unsigned int)(nch - 1));
+  }
+  __syncthreads();
+  if (!is_last) return;
+  // One device-scope acquire (an L2 invalidate, no write-back) makes the
+  // written-through partials of every block visible to ordinary loads.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // chunk statistics -> LDS; every load is issued before any is used
+  const int nst = nch * nq;
+  for (int i0 = 0; i0 < nst; i0 += 256 * 4) {
+    float mv[4], lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + tid + 256 * k;
+      if (i < nst) {
+        const float* pp = a.part + (size_t)(i / nq) * pstride + (i % nq) * (2 + kHeadDim);
+        mv[k] = pp[0];
+        lv[k] = pp[1];
+      }
     }
 #pragma unroll
-    for (int k = 0; k < 32; ++k)
-      if (c0 + k < nch) o = fmaf(fac[c0 + k], ov[k], o);
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + tid + 256 * k;
+      if (i < nst) { sm[i] = mv[k]; sf[i] = lv[k]; }
+    }
   }
-  a.attn_out[h * kHeadDim + d] = o / L;
+  __syncthreads();
+  // per head (wave h): max over the chunks, weights exp(m_c - M) into LDS,
+  // total L; lanes stride over the chunks, then a wave reduction
+  if (wv < nq) {
+    float M = -INFINITY;
+    for (int c = lane; c < nch; c += 64) M = fmaxf(M, sm[c * nq + wv]);
+    M = wave_max(M);
+    float L = 0.f;
+    for (int c = lane; c < nch; c += 64) {
+      const float f = expf(sm[c * nq + wv] - M);
+      sm[c * nq + wv] = f;
+      L = fmaf(f, sf[c * nq + wv], L);
+    }
+    L = wave_sum(L);
+    if (lane == 0) hstat[wv][1] = L;
+  }
+  __syncthreads();
+  float Lh[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) Lh[h] = h < nq ? hstat[h][1] : 1.f;
+  float acc[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) acc[h] = 0.f;
+  // branch-free: chunk indices are clamped to nch - 1 (always in bounds) and
+  // the weights of the clamped repeats are zero
+  for (int c0 = 0; c0 < nch; c0 += 16) {
+    float ov[16][NQ];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int cc = min(c0 + k, nch - 1);
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) ov[k][h] = a.part[(size_t)cc * pstride + h * (2 + kHeadDim) + 2 + tid];
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int cc = min(c0 + k, nch - 1);
+#pragma unroll
+      for (int h = 0; h < NQ; ++h) {
+        const float w = (c0 + k < nch && h < nq) ? sm[cc * nq + min(h, nq - 1)] : 0.f;
+        acc[h] = fmaf(w, ov[k][h], acc[h]);
+      }
+    }
+  }
+  for (int h = 0; h < nq; ++h) a.attn_out[h * kHeadDim + tid] = acc[h] / Lh[h];
+  if (tid == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -799,13 +903,8 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
 }
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
-  if (a.n_q < 1 || a.n_q > kMaxQHeads || grid < 1 || grid > kAttnMaxChunks) return (int)hipErrorInvalidValue;
-  hipStream_t s = (hipStream_t)stream;
-  if (a.n_q <= 4) hipLaunchKernelGGL(k_attn<4>, dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(k_attn<8>, dim3(grid), dim3(256), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(k_attn_combine, dim3(a.n_q * 4), dim3(64), 0, s, a);
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kAttnMaxChunks) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

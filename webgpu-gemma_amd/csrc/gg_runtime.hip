@@ -89,9 +89,10 @@ struct gg_ctx {
   float *qkv_out = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_out = nullptr;
   float *act = nullptr, *down_out = nullptr, *hidden = nullptr, *residual = nullptr, *normed = nullptr;
   float *logits = nullptr, *hist = nullptr, *q_dbg = nullptr;
-  float *freq_local = nullptr, *freq_global = nullptr;
+  float *rope_local = nullptr, *rope_global = nullptr;   // [ctx][cos|sin][128]
   float* cand_val = nullptr;
   uint32_t *cand_id = nullptr, *top = nullptr, *seen = nullptr;
+  unsigned int* counters = nullptr;   // attention chunk arrivals
   DevState* st = nullptr;
   int32_t* tokens = nullptr;
   int32_t* d_ids = nullptr;           // staging for gg_penalty_add
@@ -228,7 +229,7 @@ int record_forward(gg_ctx* c) {
     at.q_norm = Ly.norm[N_QN];
     at.k_norm = Ly.norm[N_KN];
     const bool swa = is_swa(c->c, l);
-    at.freq = swa ? c->freq_local : c->freq_global;
+    at.rope = swa ? c->rope_local : c->rope_global;
     at.k_cache = Ly.kc;
     at.v_cache = Ly.vc;
     at.window = swa ? c->c.sliding_window : 0;
@@ -236,6 +237,7 @@ int record_forward(gg_ctx* c) {
     at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
     at.st = c->st;
     at.part = c->attn_part;
+    at.counter = c->counters;
     at.attn_out = c->attn_out;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
@@ -354,13 +356,13 @@ gg_ctx* gg_create(const gg_config* cfg) {
   g_create_error.clear();
   if (!cfg) { set_err(nullptr, GG_ERR_INVALID, "null config"); return nullptr; }
   const gg_config& k = *cfg;
-  if (k.head_dim != kHeadDim || k.num_kv_heads != 1 || k.num_q_heads < 1 || k.num_q_heads > kMaxQHeads ||
+  if (k.head_dim != kHeadDim || k.num_kv_heads != 1 || k.num_q_heads < 1 || k.num_q_heads > kAttnMaxQ ||
       k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > 2048 || k.intermediate_size <= 0 ||
       k.intermediate_size % 64 || k.intermediate_size > kMaxK || k.vocab_size <= 0 || k.vocab_size % 64 ||
       k.num_layers <= 0 || k.context_length <= 0 || k.context_length > 32 * kAttnMaxChunks * 8 ||
       k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK) {
     set_err(nullptr, GG_ERR_INVALID,
-            "unsupported config: needs head_dim 256, one KV head, <= 8 query heads, hidden/intermediate/vocab "
+            "unsupported config: needs head_dim 256, one KV head, <= 4 query heads, hidden/intermediate/vocab "
             "multiples of 64 (hidden <= 2048, intermediate <= 8192), context <= 65536");
     return nullptr;
   }
@@ -537,7 +539,8 @@ int gg_finalize(gg_ctx* c) {
     GG_HIP(c, hipMemset(Ly.vc, 0, kvb));
   }
   GG_TRY(dalloc(c, &c->qkv_out, (size_t)c->NQKV * 4));
-  GG_TRY(dalloc(c, &c->attn_part, (size_t)kAttnMaxChunks * c->NQ * (2 + kHeadDim) * 4));
+  // sized for kAttnMaxQ heads: the merge reads whole head slots of a chunk
+  GG_TRY(dalloc(c, &c->attn_part, (size_t)kAttnMaxChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
   GG_TRY(dalloc(c, &c->attn_out, (size_t)c->QD * 4));
   GG_TRY(dalloc(c, &c->o_out, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->act, (size_t)c->I * 4));
@@ -548,16 +551,18 @@ int gg_finalize(gg_ctx* c) {
   GG_TRY(dalloc(c, &c->logits, (size_t)c->V * 4));
   GG_TRY(dalloc(c, &c->hist, (size_t)c->L * c->H * 4));
   GG_TRY(dalloc(c, &c->q_dbg, (size_t)c->L * c->QD * 4));
-  GG_TRY(dalloc(c, &c->freq_local, (kHeadDim / 2) * 4));
-  GG_TRY(dalloc(c, &c->freq_global, (kHeadDim / 2) * 4));
+  GG_TRY(dalloc(c, &c->rope_local, (size_t)c->CTX * kHeadDim * 4));
+  GG_TRY(dalloc(c, &c->rope_global, (size_t)c->CTX * kHeadDim * 4));
   GG_TRY(dalloc(c, &c->cand_val, (size_t)kSelBlocks * 256 * 4));
   GG_TRY(dalloc(c, &c->cand_id, (size_t)kSelBlocks * 256 * 4));
   GG_TRY(dalloc(c, &c->top, 512 * 4));
   GG_TRY(dalloc(c, &c->seen, (size_t)cdiv(c->V, 32) * 4));
   GG_TRY(dalloc(c, &c->st, sizeof(DevState)));
+  GG_TRY(dalloc(c, &c->counters, 256));
   GG_TRY(dalloc(c, &c->tokens, (size_t)c->CTX * 4));
   GG_TRY(dalloc(c, &c->d_ids, (size_t)c->CTX * 4));
   GG_HIP(c, hipMemset(c->st, 0, sizeof(DevState)));
+  GG_HIP(c, hipMemset(c->counters, 0, 256));
   GG_HIP(c, hipMemset(c->seen, 0, (size_t)cdiv(c->V, 32) * 4));
   GG_HIP(c, hipMemset(c->tokens, 0, (size_t)c->CTX * 4));
   GG_HIP(c, hipMemset(c->attn_out, 0, (size_t)c->QD * 4));
@@ -565,16 +570,28 @@ int gg_finalize(gg_ctx* c) {
   GG_HIP(c, hipMemset(c->normed, 0, (size_t)c->H * 4));
   GG_HIP(c, hipMemset(c->logits, 0, (size_t)c->V * 4));
 
-  // RoPE inverse frequencies, computed once on the host exactly as the WGSL
-  // expression 1.0 / pow(theta, f32(2i) / f32(head_dim)) (shaders.ts:457).
-  float fl[kHeadDim / 2], fg[kHeadDim / 2];
-  for (int i = 0; i < kHeadDim / 2; ++i) {
-    const float e = (float)(i * 2) / (float)kHeadDim;
-    fl[i] = 1.0f / powf(c->c.rope_theta_local, e);
-    fg[i] = 1.0f / powf(c->c.rope_theta_global, e);
+  // RoPE tables, computed once on the host exactly as the WGSL expressions
+  // freq = 1.0 / pow(theta, f32(2i) / f32(head_dim)), angle = f32(pos) *
+  // freq, cos(angle), sin(angle) (shaders.ts:457-460), for every position.
+  {
+    std::vector<float> tl((size_t)c->CTX * kHeadDim), tg((size_t)c->CTX * kHeadDim);
+    float fl[kHeadDim / 2], fg[kHeadDim / 2];
+    for (int i = 0; i < kHeadDim / 2; ++i) {
+      const float e = (float)(i * 2) / (float)kHeadDim;
+      fl[i] = 1.0f / powf(c->c.rope_theta_local, e);
+      fg[i] = 1.0f / powf(c->c.rope_theta_global, e);
+    }
+    for (int p = 0; p < c->CTX; ++p)
+      for (int i = 0; i < kHeadDim / 2; ++i) {
+        const float al = (float)p * fl[i], ag = (float)p * fg[i];
+        tl[(size_t)p * kHeadDim + i] = cosf(al);
+        tl[(size_t)p * kHeadDim + kHeadDim / 2 + i] = sinf(al);
+        tg[(size_t)p * kHeadDim + i] = cosf(ag);
+        tg[(size_t)p * kHeadDim + kHeadDim / 2 + i] = sinf(ag);
+      }
+    GG_HIP(c, hipMemcpy(c->rope_local, tl.data(), tl.size() * 4, hipMemcpyHostToDevice));
+    GG_HIP(c, hipMemcpy(c->rope_global, tg.data(), tg.size() * 4, hipMemcpyHostToDevice));
   }
-  GG_HIP(c, hipMemcpy(c->freq_local, fl, sizeof(fl), hipMemcpyHostToDevice));
-  GG_HIP(c, hipMemcpy(c->freq_global, fg, sizeof(fg), hipMemcpyHostToDevice));
 
   GG_HIP(c, hipHostMalloc((void**)&c->h_st, sizeof(DevState), hipHostMallocDefault));
   GG_HIP(c, hipHostMalloc((void**)&c->h_tokens, (size_t)c->CTX * 4, hipHostMallocDefault));
