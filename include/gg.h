@@ -67,6 +67,9 @@ typedef struct gg_config {
   int32_t swa_period;       /* isSwaLayer(il) = il % swa_period < swa_period - 1 (types.ts:38-40) */
   int32_t sliding_window;   /* 0 = full attention */
   int32_t attention_mode;   /* GG_ATTN_* (documentation of intent; window/theta decide) */
+  int32_t prefill_batch;    /* 0: gg_prefill runs the decode pass per token like the reference
+                               (engine.ts:923-928); > 0: prompt rows per batched MFMA prefill
+                               slice (no reference counterpart) */
 } gg_config;
 
 /* Sampling options of one selection (GenerateOptions, types.ts:65-78), kept
@@ -97,9 +100,11 @@ int gg_upload_tensor(gg_ctx* ctx, const char* name, uint32_t ggml_type, const ui
  * captures the per-token HIP graphs. */
 int gg_finalize(gg_ctx* ctx);
 
-/* Replaces prefillBatched / forwardPassOnly (engine.ts:917-928): one forward
- * pass per token at positions start_pos.., no LM head; returns after the
- * device has finished (onSubmittedWorkDone). */
+/* Replaces prefillBatched / forwardPassOnly (engine.ts:917-928): the tokens
+ * at positions start_pos.. go through every layer (KV cache written), no LM
+ * head; the last token's normed hidden is left for gg_select. Returns after
+ * the device has finished (onSubmittedWorkDone). With prefill_batch > 0 and
+ * n > 1 the prompt runs as M-row GEMMs on MFMA plus batched attention. */
 int gg_prefill(gg_ctx* ctx, const int32_t* tokens, int32_t n, int32_t start_pos);
 
 /* Replaces getFirstTokenAfterPrefill / sampleNextToken (engine.ts:805-902,

@@ -32,12 +32,12 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layouts_match_header():
-    assert ctypes.sizeof(capi.GGConfig) == 14 * 4
+    assert ctypes.sizeof(capi.GGConfig) == 15 * 4
     assert ctypes.sizeof(capi.GGSample) == 3 * 8
 
 
 def test_create_rejects_bad_config_without_touching_a_device():
-    cfg = capi.GGConfig(1152, 26, 4, 1, 128, 6912, 262144, 2048, 1e-6, 1e6, 1e6, 6, 0, 0)  # head_dim 128
+    cfg = capi.GGConfig(1152, 26, 4, 1, 128, 6912, 262144, 2048, 1e-6, 1e6, 1e6, 6, 0, 0, 0)  # head_dim 128
     lib = capi.lib()
     assert not lib.gg_create(ctypes.byref(cfg))
     assert b"head_dim" in lib.gg_last_error(None)

@@ -1,0 +1,102 @@
+"""Batched prefill (M-row GEMMs on fp32 MFMA + batched attention) against the
+oracle's token-by-token prefill (engine.ts:923-928) and against the GPU's own
+per-token path at the Gemma-3-1B shape."""
+import numpy as np
+import pytest
+
+from gemma_amd import capi, synth
+from oracle import oracle as orc
+
+from gpu_util import rel, say
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+_MODELS = {}
+
+
+def engine(shape, tensors, batch):
+    e = capi.Engine(shape.gg_config(prefill_batch=batch))
+    e.upload_model(tensors)
+    e.finalize()
+    return e
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    return synth.make_model(synth.TINY, seed=7)
+
+
+@pytest.mark.parametrize("mode,batch,n", [("reference", 64, 40), ("gemma3", 64, 40), ("gemma3", 16, 53),
+                                          ("gemma3", 256, 200)])
+def test_tiny_batched_prefill_matches_oracle(gpu, tiny_model, mode, batch, n):
+    shape = synth.TINY.reference_mode() if mode == "reference" else synth.TINY.gemma3_mode(window=9)
+    say("tiny batched prefill", mode, batch, n)
+    e = engine(shape, tiny_model, batch)
+    o = orc.OracleModel(shape, tiny_model)
+    prompt = synth.prompt_ids(n, seed=21, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    for l in range(shape.layers):
+        assert rel(e.read(capi.READ_LAYER_HIDDEN, l), o.buffer(orc.GOR_LAYER_HIDDEN, l)) < TOL, l
+        kc = e.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:n]
+        vc = e.read(capi.READ_V_CACHE, l).reshape(shape.ctx, 256)[:n]
+        assert rel(kc, o.buffer(orc.GOR_K_CACHE, l).reshape(shape.ctx, 256)[:n]) < TOL, l
+        assert rel(vc, o.buffer(orc.GOR_V_CACHE, l).reshape(shape.ctx, 256)[:n]) < TOL, l
+    assert rel(e.read(capi.READ_NORMED), o.buffer(orc.GOR_NORMED)) < TOL
+    tok = e.select()
+    assert tok == o.select()
+    # decode continues from the batched prefill exactly like from the oracle's
+    pos = n
+    for _ in range(6):
+        nxt = e.step(tok, pos)
+        o.forward(tok, pos)
+        assert nxt == o.select()
+        tok, pos = nxt, pos + 1
+    e.close()
+
+
+def test_tiny_second_turn_batched(gpu, tiny_model):
+    # a second prefill continues at kvPosition (engine.ts:988-990)
+    shape = synth.TINY.gemma3_mode(window=7)
+    e = engine(shape, tiny_model, 32)
+    o = orc.OracleModel(shape, tiny_model)
+    a = synth.prompt_ids(20, seed=1, vocab=shape.vocab)
+    b = synth.prompt_ids(15, seed=2, vocab=shape.vocab)
+    e.prefill(a, 0)
+    e.prefill(b, 20)
+    o.prefill(a, 0)
+    o.prefill(b, 20)
+    assert rel(e.read(capi.READ_NORMED), o.buffer(orc.GOR_NORMED)) < TOL
+    assert e.select() == o.select()
+    e.close()
+
+
+@pytest.mark.parametrize("mode", ["gemma3", "reference"])
+def test_1b_batched_prefill_2048_matches_token_by_token(gpu, mode):
+    shape = synth.GEMMA3_1B.with_ctx(4096)
+    shape = shape.gemma3_mode() if mode == "gemma3" else shape.reference_mode()
+    say("1b batched prefill", mode)
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    prompt = synth.prompt_ids(2048, seed=2048, vocab=shape.vocab)
+    a = engine(shape, t, 2048)
+    a.prefill(prompt, 0)
+    b = engine(shape, t, 0)
+    b.prefill(prompt, 0)
+    say("1b prefilled both")
+    for l in range(shape.layers):
+        assert rel(a.read(capi.READ_LAYER_HIDDEN, l), b.read(capi.READ_LAYER_HIDDEN, l)) < TOL, l
+    for l in (0, 5, 13, 25):
+        assert rel(a.read(capi.READ_K_CACHE, l), b.read(capi.READ_K_CACHE, l)) < TOL, l
+        assert rel(a.read(capi.READ_V_CACHE, l), b.read(capi.READ_V_CACHE, l)) < TOL, l
+    ta, tb = a.select(), b.select()
+    assert rel(a.read(capi.READ_LOGITS), b.read(capi.READ_LOGITS)) < TOL
+    assert ta == tb
+    pos = 2048
+    for _ in range(8):
+        ta, tb = a.step(ta, pos), b.step(tb, pos)
+        assert ta == tb
+        pos += 1
+    a.close()
+    b.close()

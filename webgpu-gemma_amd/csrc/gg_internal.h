@@ -91,7 +91,7 @@ struct GemvArgs {
 };
 
 struct AttnArgs {
-  const float* qkv;        // [n_q*256 + 512] QKV projection output
+  const float* qkv;        // [n_q*256 + 512] QKV projection output (prefill: row stride)
   int n_q;                 // query heads (one KV head)
   const float* q_norm;     // [256]
   const float* k_norm;     // [256]
@@ -106,6 +106,43 @@ struct AttnArgs {
   unsigned int* counter;   // arrivals of the chunk blocks (reset by the last)
   float* attn_out;         // [n_q * 256]
   float* q_dbg;            // optional: normed+roped q of this token
+  // batched prefill (k_attn<true>): query row r = blockIdx.y sits at position
+  // pf_start + r; K/V of every prompt position are already in the cache
+  int pf_start;
+  int max_chunks;          // chunk limit per query (kAttnMaxChunks for decode)
+};
+
+// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W pair-interleaved (CI = 8).
+struct GemmArgs {
+  const float* A;          // [M][K] row-major activations
+  const uint8_t* W;
+  int M, N, K, Kp, KpS;
+  float* C;                // [M][N] (EPI_OUT) or act [M][N/2] (EPI_GEGLU)
+};
+
+// Row-wise prefill helpers: one block per prompt row.
+struct RowArgs {
+  int M, H;
+  float eps;
+  int pf_start;
+  const int32_t* tokens;   // EMBED: prompt ids
+  const uint8_t* embd;
+  int embd_KpS;
+  float embed_scale;
+  const float* pre;        // RESID: output of the previous GEMM [M][H]
+  const float* res;        // RESID: residual stream entering the add [M][H]
+  const float* w_post;
+  const float* w_pre;
+  float* res_out;          // [M][H] new residual stream
+  float* x_out;            // [M][H] normed GEMM input
+  float* last_hidden;      // optional: row M-1 of res_out (per-layer history)
+  // KV: k/v of each row into the cache
+  const float* qkv;
+  int n_q;
+  const float* k_norm;
+  const float* rope;
+  float* k_cache;
+  float* v_cache;
 };
 
 struct FinalArgs {
@@ -144,5 +181,11 @@ int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long
                   long long dst_row_offset, int interleave_half, void* stream);
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
 int launch_seen_add(uint32_t* seen, DevState* st, const int32_t* ids, int n, int V, void* stream);
+int launch_prefill_attention(const AttnArgs& a, int M, void* stream);
+int launch_gemm(int epi, const GemmArgs& a, void* stream);
+int launch_rows_embed(const RowArgs& a, void* stream);
+int launch_rows_resid(const RowArgs& a, void* stream);
+int launch_rows_kv(const RowArgs& a, void* stream);
+constexpr int kPrefillChunks = 16;   // chunks per query in the batched prefill
 
 }  // namespace gg

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 __device__ __forceinline__ void attn_span(const AttnArgs& a, int pos, int* t_lo, int* ch, int* nch) {
   const int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
   const int span = pos - lo + 1;
-  const int c = kAttnChunk * ((span + kAttnChunk * kAttnMaxChunks - 1) / (kAttnChunk * kAttnMaxChunks));
+  const int c = kAttnChunk * ((span + kAttnChunk * a.max_chunks - 1) / (kAttnChunk * a.max_chunks));
   *t_lo = lo;
   *ch = c;
   *nch = (span + c - 1) / c;
@@ -309,6 +309,10 @@ constexpr int kAttnP = 8;   // positions per wave pass
 constexpr int kQPad = 288;  // LDS floats per head: 8 octants of 32 dims + 4 pad each
 __device__ __forceinline__ int qidx(int d) { return (d >> 5) * 36 + (d & 31); }
 
+// PF = false: decode, one token at DevState.pos; the block holding pos also
+// norms/ropes k and stores k/v. PF = true: batched prefill, query row
+// blockIdx.y at pf_start + blockIdx.y, every K/V row already in the cache.
+template <bool PF>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   constexpr int NQ = kAttnMaxQ;
   __shared__ float qs[NQ][kQPad];
@@ -324,14 +328,20 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
-  const int pos = a.st->pos;
+  const int nqd = nq * kHeadDim;
+  const int row = PF ? (int)blockIdx.y : 0;
+  const int pos = PF ? a.pf_start + row : a.st->pos;
+  const float* qkv = a.qkv + (size_t)row * (nqd + 2 * kHeadDim);
+  float* part = a.part + (size_t)row * a.max_chunks * kAttnMaxQ * (2 + kHeadDim);
+  unsigned int* counter = a.counter + row;
+  float* attn_out = a.attn_out + (size_t)row * nqd;
   int t_lo, ch, nch;
   attn_span(a, pos, &t_lo, &ch, &nch);
   const int b = blockIdx.x;
   if (b >= nch) return;
   const int t0 = t_lo + b * ch;
   const int t1 = min(t0 + ch, pos + 1);
-  const int nqd = nq * kHeadDim;
+  const int kv_end = PF ? pos + 1 : pos;   // rows [.., kv_end) come from the cache
   const int pl = lane >> 3, oc = lane & 7;
 
   // 0. loads that do not depend on q: this wave's first pass of K rows (lane
@@ -341,7 +351,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   float4 kr[8], vr[kAttnP];
   {
     const int t = tb0 + pl;
-    if (t < pos && t < t1) {
+    if (t < kv_end && t < t1) {
       const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = kp[j];
@@ -349,17 +359,17 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kAttnP; ++i) {
       const int tv = tb0 + i;
-      if (tv < pos && tv < t1) vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
+      if (tv < kv_end && tv < t1) vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
     }
   }
   const bool my_head = wv < nq;
-  const bool k_head = (wv == 0) && (b == nch - 1);
+  const bool k_head = !PF && (wv == 0) && (b == nch - 1);
   float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    hx[i] = my_head ? a.qkv[wv * kHeadDim + lane + 64 * i] : 0.f;
+    hx[i] = my_head ? qkv[wv * kHeadDim + lane + 64 * i] : 0.f;
     nwt[i] = a.q_norm[lane + 64 * i];
-    kx[i] = a.qkv[nqd + lane + 64 * i];
+    kx[i] = PF ? 0.f : qkv[nqd + lane + 64 * i];
     kwt[i] = a.k_norm[lane + 64 * i];
   }
   // RoPE table row of this position: cos(f32(pos) * freq[i]), sin(...)
@@ -369,7 +379,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     cs[j] = rt[lane + 64 * j];
     sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
   }
-  if (tid < kHeadDim) vs[tid] = a.qkv[nqd + kHeadDim + tid];
+  if (!PF && tid < kHeadDim) vs[tid] = qkv[nqd + kHeadDim + tid];
 
   // 1. wave w: RMSNorm + NEOX RoPE of query head w (and, in the block that
   // holds `pos`, wave 0 also of the key head) -- fusedPerHeadNormRope,
@@ -398,11 +408,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   if (k_head) norm_rope(kx, kwt, ks);
   __syncthreads();
 
-  if (b == nch - 1) {
+  if (!PF && b == nch - 1) {
     a.k_cache[(size_t)pos * kHeadDim + tid] = ks[qidx(tid)];
     a.v_cache[(size_t)pos * kHeadDim + tid] = vs[tid];
   }
-  if (b == 0 && a.q_dbg)
+  if (!PF && b == 0 && a.q_dbg)
     for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = qs[e >> 8][qidx(e & 255)];
 
   // q slice of this lane's score layout: 4 heads x 32 dims in registers
@@ -423,20 +433,20 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   }
   for (int tb = tb0; tb < t1; tb += 4 * kAttnP) {
     const int t = tb + pl;
-    if (tb != tb0 && t < pos && t < t1) {
+    if (tb != tb0 && t < kv_end && t < t1) {
       const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = kp[j];
     }
-    if (t == pos) {
+    if (!PF && t == pos) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = *(const float4*)&ks[36 * oc + 4 * j];
     }
 #pragma unroll
     for (int i = 0; i < kAttnP; ++i) {
       const int tv = tb + i;
-      if (tv == pos) vr[i] = *(const float4*)&vs[4 * lane];
-      else if (tb != tb0 && tv < pos && tv < t1)
+      if (!PF && tv == pos) vr[i] = *(const float4*)&vs[4 * lane];
+      else if (tb != tb0 && tv < kv_end && tv < t1)
         vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
     }
     const bool valid = t < t1;
@@ -536,10 +546,10 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   }
   if (nch == 1) {   // a single chunk is the result
     __syncthreads();
-    for (int h = 0; h < nq; ++h) a.attn_out[h * kHeadDim + tid] = O[h] / hstat[h][1];
+    for (int h = 0; h < nq; ++h) attn_out[h * kHeadDim + tid] = O[h] / hstat[h][1];
     return;
   }
-  float* mypart = a.part + (size_t)b * pstride;
+  float* mypart = part + (size_t)b * pstride;
   for (int h = 0; h < nq; ++h) st_dev(mypart + h * (2 + kHeadDim) + 2 + tid, O[h]);
   __syncthreads();
   if (tid < nq) {
@@ -553,7 +563,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const unsigned int old = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = (old == (unsigned int)(nch - 1));
   }
   __syncthreads();
@@ -569,7 +579,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     for (int k = 0; k < 4; ++k) {
       const int i = i0 + tid + 256 * k;
       if (i < nst) {
-        const float* pp = a.part + (size_t)(i / nq) * pstride + (i % nq) * (2 + kHeadDim);
+        const float* pp = part + (size_t)(i / nq) * pstride + (i % nq) * (2 + kHeadDim);
         mv[k] = pp[0];
         lv[k] = pp[1];
       }
@@ -611,7 +621,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     for (int k = 0; k < 16; ++k) {
       const int cc = min(c0 + k, nch - 1);
 #pragma unroll
-      for (int h = 0; h < NQ; ++h) ov[k][h] = a.part[(size_t)cc * pstride + h * (2 + kHeadDim) + 2 + tid];
+      for (int h = 0; h < NQ; ++h) ov[k][h] = part[(size_t)cc * pstride + h * (2 + kHeadDim) + 2 + tid];
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -623,8 +633,8 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
       }
     }
   }
-  for (int h = 0; h < nq; ++h) a.attn_out[h * kHeadDim + tid] = acc[h] / Lh[h];
-  if (tid == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int h = 0; h < nq; ++h) attn_out[h * kHeadDim + tid] = acc[h] / Lh[h];
+  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -814,6 +824,188 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 }
 
 // ---------------------------------------------------------------------------
+// Batched prefill (no reference counterpart: the reference runs the decode
+// pass once per prompt token, engine.ts:923-928).
+//
+// k_gemm: C[M x N] = A[M x K] * W[N x K]^T on fp32 MFMA (v_mfma_f32_16x16x4f32)
+// with W's Q8_0 pairs dequantised exactly (q * d is exact in f32) into LDS,
+// so the products match the decode GEMV's up to summation order. Block tile
+// 64 (rows) x 128 (features) x 64 (one pair column); wave w owns a 32 x 64
+// sub-tile (2 x 4 MFMA tiles). Next stage's global loads are issued before
+// the current stage's MFMAs.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kGBM = 64, kGBN = 128, kGStr = 68;
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+  __shared__ float As[kGBM][kGStr];
+  __shared__ float Bs[kGBN][kGStr];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
+  const int wm = (wv >> 1) * 32, wn = (wv & 1) * 64;
+  // A loader: row tid/4, 16 k at (tid%4)*16; W loader (tid < 128): row n0+tid
+  const int ar = tid >> 2, ak = (tid & 3) * 16;
+  const float* arow = a.A + (size_t)min(m0 + ar, a.M - 1) * a.K + ak;
+  const int wn_row = n0 + (tid & 127);
+  const uint8_t* wbase = a.W + (((size_t)(wn_row >> 3) * a.KpS) * 64 + (wn_row & 7)) * kPairBytes;
+  auto wpair = [&](int c) { return wbase + ((size_t)(c >> 3) * 64 + (c & 7) * 8) * kPairBytes; };
+
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  float4 av[4];
+  Pair wp;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + 4 * q);
+  if (tid < 128) load_pair(wpair(0), wp);
+
+  for (int c = 0; c < a.Kp; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *(float4*)&As[ar][ak + 4 * q] = av[q];
+    if (tid < 128) {
+      const float d0 = f16_lo(wp.w[0]), d1 = f16_hi(wp.w[8]);
+      float* br = Bs[tid];
+#pragma unroll
+      for (int j = 0; j < 32; j += 4) {
+        float4 v0, v1;
+        v0.x = sbyte(wp.w[(2 + j) >> 2], (2 + j) & 3) * d0;
+        v0.y = sbyte(wp.w[(3 + j) >> 2], (3 + j) & 3) * d0;
+        v0.z = sbyte(wp.w[(4 + j) >> 2], (4 + j) & 3) * d0;
+        v0.w = sbyte(wp.w[(5 + j) >> 2], (5 + j) & 3) * d0;
+        v1.x = sbyte(wp.w[9 + (j >> 2)], 0) * d1;
+        v1.y = sbyte(wp.w[9 + (j >> 2)], 1) * d1;
+        v1.z = sbyte(wp.w[9 + (j >> 2)], 2) * d1;
+        v1.w = sbyte(wp.w[9 + (j >> 2)], 3) * d1;
+        *(float4*)&br[j] = v0;
+        *(float4*)&br[32 + j] = v1;
+      }
+    }
+    __syncthreads();
+    if (c + 1 < a.Kp) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + (size_t)(c + 1) * 64 + 4 * q);
+      if (tid < 128) load_pair(wpair(c + 1), wp);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 64; kk += 4) {
+      float af[2], bf[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = As[wm + i * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = Bs[wn + j * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // D[i][j] of a 16x16 tile: lane l, register r -> row 4 (l / 16) + r, col l % 16
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm + i * 16 + 4 * (lane >> 4) + r;
+        const int n = n0 + wn + j * 16 + (lane & 15);
+        const float v = acc[i][j][r];
+        if (EPI == EPI_OUT) {
+          if (m < a.M) a.C[(size_t)m * a.N + n] = v;
+        } else {
+          // fused gate/up rows: 4 gate rows then their 4 up rows per group of 8
+          const float up = __shfl(v, lane + 4, 64);
+          if (m < a.M && (n & 4) == 0) a.C[(size_t)m * (a.N / 2) + (n >> 3) * 4 + (n & 3)] = gelu_mul(v, up);
+        }
+      }
+}
+
+// Row kernels (one block per prompt row, H <= 2048).
+__device__ __forceinline__ void row_norm_out(const float* r, const float* w, int H, float eps, float* out,
+                                             float* sh4, int n) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) ss = fmaf(r[i], r[i], ss);
+  const float rms = sqrtf(block_sum256(ss, sh4) / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) out[threadIdx.x + 256 * i] = (r[i] * w[threadIdx.x + 256 * i]) / rms;
+}
+
+__global__ __launch_bounds__(256) void k_rows_embed(RowArgs a) {
+  __shared__ float sh4[4];
+  const int row = blockIdx.x, tid = threadIdx.x, H = a.H;
+  const int n = (H - tid + 255) / 256;
+  const int token = a.tokens[row];
+  float h[8];
+  GemvArgs g{};
+  g.embd = a.embd;
+  g.embd_KpS = a.embd_KpS;
+  g.embed_scale = a.embed_scale;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+      h[i] = embed_elem(g, token, tid + 256 * i);
+      a.res_out[(size_t)row * H + tid + 256 * i] = h[i];
+    }
+  row_norm_out(h, a.w_pre, H, a.eps, a.x_out + (size_t)row * H, sh4, n);
+}
+
+__global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
+  __shared__ float sh4[4];
+  const int row = blockIdx.x, tid = threadIdx.x, H = a.H;
+  const int n = (H - tid + 255) / 256;
+  const size_t o = (size_t)row * H;
+  float v[8], rs[8], wq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+      v[i] = a.pre[o + tid + 256 * i];
+      rs[i] = a.res[o + tid + 256 * i];
+      wq[i] = a.w_post[tid + 256 * i];
+    }
+  float s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) s1 = fmaf(v[i], v[i], s1);
+  const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+      v[i] = rs[i] + (v[i] * wq[i]) / rms1;
+      a.res_out[o + tid + 256 * i] = v[i];
+      if (a.last_hidden && row == a.M - 1) a.last_hidden[tid + 256 * i] = v[i];
+    }
+  row_norm_out(v, a.w_pre, H, a.eps, a.x_out + o, sh4, n);
+}
+
+// k of each prompt row: per-head RMSNorm + NEOX RoPE, then k and v into the
+// cache at pf_start + row (fusedPerHeadNormRope + kvCacheStore).
+__global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
+  __shared__ float sh4[4];
+  __shared__ float kk[kHeadDim];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int pos = a.pf_start + row;
+  const float* q = a.qkv + (size_t)row * (a.n_q * kHeadDim + 2 * kHeadDim) + a.n_q * kHeadDim;
+  const float k = q[tid], v = q[kHeadDim + tid], w = a.k_norm[tid];
+  const float* rt = a.rope + (size_t)pos * kHeadDim;
+  const float cs = rt[tid & 127], sn = rt[128 + (tid & 127)];
+  const float rms = sqrtf(block_sum256(k * k, sh4) / (float)kHeadDim + a.eps);
+  kk[tid] = (k * w) / rms;
+  __syncthreads();
+  float out;
+  if (tid < 128) out = kk[tid] * cs - kk[tid + 128] * sn;
+  else out = kk[tid - 128] * sn + kk[tid] * cs;
+  a.k_cache[(size_t)pos * kHeadDim + tid] = out;
+  a.v_cache[(size_t)pos * kHeadDim + tid] = v;
+}
+
+// ---------------------------------------------------------------------------
 // Upload helpers.
 // k_repack: GGUF row-major Q8_0 (rows of Kp 68-byte pairs) -> the
 // pair-interleaved layout L. interleave_half > 0 places source row r at fused
@@ -903,8 +1095,15 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
 }
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
-  if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kAttnMaxChunks) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kAttnMaxChunks || a.max_chunks != kAttnMaxChunks)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_prefill_attention(const AttnArgs& a, int M, void* stream) {
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || M < 1 || a.max_chunks != kPrefillChunks) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn<true>, dim3(kPrefillChunks, M), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
@@ -937,6 +1136,32 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
   if (n <= 0) return 0;
   hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src, out,
                      n);
+  return (int)hipGetLastError();
+}
+
+int launch_gemm(int epi, const GemmArgs& a, void* stream) {
+  if (a.M < 1 || a.N % kGBN || a.K != a.Kp * 64 || a.KpS != (a.Kp + 7) / 8) return (int)hipErrorInvalidValue;
+  dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM);
+  if (epi == EPI_OUT) hipLaunchKernelGGL(k_gemm<EPI_OUT>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(k_gemm<EPI_GEGLU>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_rows_embed(const RowArgs& a, void* stream) {
+  if (a.H > 2048 || a.M < 1) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_embed, dim3(a.M), dim3(256), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_rows_resid(const RowArgs& a, void* stream) {
+  if (a.H > 2048 || a.M < 1) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_resid, dim3(a.M), dim3(256), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_rows_kv(const RowArgs& a, void* stream) {
+  if (a.M < 1) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_kv, dim3(a.M), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

@@ -100,6 +100,12 @@ struct gg_ctx {
   size_t staging_bytes = 0;
   int attn_grid = 1;
 
+  // batched prefill (prefill_batch > 0)
+  int pf_M = 0;
+  float *pf_hidden = nullptr, *pf_residual = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
+  float *pf_o = nullptr, *pf_act = nullptr, *pf_part = nullptr;
+  unsigned int* pf_counters = nullptr;
+
   // pinned host mirrors
   DevState* h_st = nullptr;
   int32_t* h_tokens = nullptr;
@@ -239,6 +245,7 @@ int record_forward(gg_ctx* c) {
     at.part = c->attn_part;
     at.counter = c->counters;
     at.attn_out = c->attn_out;
+    at.max_chunks = kAttnMaxChunks;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
       ProbeScope ps(c, GG_PROBE_ATTN, l);
@@ -348,6 +355,109 @@ int sync(gg_ctx* c, const char* what) {
   return GG_OK;
 }
 
+
+GemmArgs gemm_base(const float* A, const uint8_t* W, const Q8Layout& L, int M, float* C) {
+  GemmArgs g{};
+  g.A = A;
+  g.W = W;
+  g.M = M;
+  g.N = L.rows;
+  g.K = L.K;
+  g.Kp = L.Kp;
+  g.KpS = L.KpS;
+  g.C = C;
+  return g;
+}
+
+// Batched prefill of prompt rows [start, start + M): per layer QKV GEMM, k/v
+// into the cache, batched attention, O GEMM, residual + norms, gate/up GEMM
+// with GeGLU, down GEMM, residual + next norm; the last row ends like k_final.
+int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
+  const float eps = c->c.rms_norm_eps;
+  hipStream_t s = c->stream;
+  RowArgs r{};
+  r.M = M;
+  r.H = c->H;
+  r.eps = eps;
+  r.pf_start = start;
+  r.tokens = d_tokens;
+  r.embd = c->embd;
+  r.embd_KpS = c->lay_embd.KpS;
+  r.embed_scale = sqrtf((float)c->H);
+  r.w_pre = c->layers[0].norm[N_ATTN];
+  r.res_out = c->pf_hidden;
+  r.x_out = c->pf_xn;
+  GG_TRY(launch_rc(c, launch_rows_embed(r, s), "prefill embed"));
+  for (int l = 0; l < c->L; ++l) {
+    Layer& Ly = c->layers[l];
+    const bool swa = is_swa(c->c, l);
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_xn, Ly.qkv, c->lay_qkv, M, c->pf_qkv), s), "prefill qkv"));
+    RowArgs kv{};
+    kv.M = M;
+    kv.eps = eps;
+    kv.pf_start = start;
+    kv.qkv = c->pf_qkv;
+    kv.n_q = c->NQ;
+    kv.k_norm = Ly.norm[N_KN];
+    kv.rope = swa ? c->rope_local : c->rope_global;
+    kv.k_cache = Ly.kc;
+    kv.v_cache = Ly.vc;
+    GG_TRY(launch_rc(c, launch_rows_kv(kv, s), "prefill kv"));
+    AttnArgs at{};
+    at.qkv = c->pf_qkv;
+    at.n_q = c->NQ;
+    at.q_norm = Ly.norm[N_QN];
+    at.k_norm = Ly.norm[N_KN];
+    at.rope = kv.rope;
+    at.k_cache = Ly.kc;
+    at.v_cache = Ly.vc;
+    at.window = swa ? c->c.sliding_window : 0;
+    at.eps = eps;
+    at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
+    at.part = c->pf_part;
+    at.counter = c->pf_counters;
+    at.attn_out = c->pf_attn;
+    at.pf_start = start;
+    at.max_chunks = kPrefillChunks;
+    GG_TRY(launch_rc(c, launch_prefill_attention(at, M, s), "prefill attention"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_attn, Ly.o, c->lay_o, M, c->pf_o), s), "prefill o"));
+    RowArgs r1 = r;
+    r1.pre = c->pf_o;
+    r1.res = c->pf_hidden;
+    r1.w_post = Ly.norm[N_POST_ATTN];
+    r1.w_pre = Ly.norm[N_FFN];
+    r1.res_out = c->pf_residual;
+    r1.x_out = c->pf_xn;
+    GG_TRY(launch_rc(c, launch_rows_resid(r1, s), "prefill post-attn"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_GEGLU, gemm_base(c->pf_xn, Ly.gu, c->lay_gu, M, c->pf_act), s), "prefill gate/up"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_act, Ly.down, c->lay_down, M, c->pf_o), s), "prefill down"));
+    if (l + 1 < c->L) {
+      RowArgs r2 = r;
+      r2.pre = c->pf_o;
+      r2.res = c->pf_residual;
+      r2.w_post = Ly.norm[N_POST_FFW];
+      r2.w_pre = c->layers[l + 1].norm[N_ATTN];
+      r2.res_out = c->pf_hidden;
+      r2.x_out = c->pf_xn;
+      r2.last_hidden = c->hist + (size_t)l * c->H;
+      GG_TRY(launch_rc(c, launch_rows_resid(r2, s), "prefill post-ffn"));
+    } else {
+      FinalArgs f{};
+      f.pre_vec = c->pf_o + (size_t)(M - 1) * c->H;
+      f.pre_res = c->pf_residual + (size_t)(M - 1) * c->H;
+      f.w_post = Ly.norm[N_POST_FFW];
+      f.w_out = c->out_norm;
+      f.hidden = c->hidden;
+      f.hist_out = c->hist + (size_t)l * c->H;
+      f.normed = c->normed;
+      f.H = c->H;
+      f.eps = eps;
+      f.st = c->st;
+      GG_TRY(launch_rc(c, launch_final(f, s), "prefill final"));
+    }
+  }
+  return GG_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -563,6 +673,21 @@ int gg_finalize(gg_ctx* c) {
   GG_TRY(dalloc(c, &c->d_ids, (size_t)c->CTX * 4));
   GG_HIP(c, hipMemset(c->st, 0, sizeof(DevState)));
   GG_HIP(c, hipMemset(c->counters, 0, 256));
+  if (c->c.prefill_batch > 0) {
+    const int M = std::min(c->c.prefill_batch, c->CTX);
+    c->pf_M = M;
+    const size_t MH = (size_t)M * c->H * 4;
+    GG_TRY(dalloc(c, &c->pf_hidden, MH));
+    GG_TRY(dalloc(c, &c->pf_residual, MH));
+    GG_TRY(dalloc(c, &c->pf_xn, MH));
+    GG_TRY(dalloc(c, &c->pf_o, MH));
+    GG_TRY(dalloc(c, &c->pf_qkv, (size_t)M * c->NQKV * 4));
+    GG_TRY(dalloc(c, &c->pf_attn, (size_t)M * c->QD * 4));
+    GG_TRY(dalloc(c, &c->pf_act, (size_t)M * c->I * 4));
+    GG_TRY(dalloc(c, &c->pf_part, (size_t)M * kPrefillChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
+    GG_TRY(dalloc(c, &c->pf_counters, (size_t)M * 4));
+    GG_HIP(c, hipMemset(c->pf_counters, 0, (size_t)M * 4));
+  }
   GG_HIP(c, hipMemset(c->seen, 0, (size_t)cdiv(c->V, 32) * 4));
   GG_HIP(c, hipMemset(c->tokens, 0, (size_t)c->CTX * 4));
   GG_HIP(c, hipMemset(c->attn_out, 0, (size_t)c->QD * 4));
@@ -624,6 +749,14 @@ int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
   c->h_st->cursor = 0;
   GG_HIP(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
   GG_TRY(push_state(c, 0, offsetof(DevState, temperature)));
+  if (c->pf_M > 0 && n > 1) {
+    for (int s0 = 0; s0 < n; s0 += c->pf_M) {
+      const int M = std::min(c->pf_M, n - s0);
+      GG_TRY(prefill_slice(c, c->tokens + s0, M, start_pos + s0));
+    }
+    c->timed = false;
+    return sync(c, "prefill");
+  }
   for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
   c->timed = false;
   return sync(c, "prefill");

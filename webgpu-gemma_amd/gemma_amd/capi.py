@@ -58,6 +58,7 @@ class GGConfig(ctypes.Structure):
         ("swa_period", ctypes.c_int32),
         ("sliding_window", ctypes.c_int32),
         ("attention_mode", ctypes.c_int32),
+        ("prefill_batch", ctypes.c_int32),
     ]
 
 

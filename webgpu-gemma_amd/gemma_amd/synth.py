@@ -54,10 +54,10 @@ class Shape:
     def with_ctx(self, ctx: int) -> "Shape":
         return replace(self, ctx=ctx)
 
-    def gg_config(self) -> capi.GGConfig:
+    def gg_config(self, prefill_batch: int = 0) -> capi.GGConfig:
         return capi.GGConfig(self.hidden, self.layers, self.n_q, self.n_kv, self.head_dim, self.inter, self.vocab,
                              self.ctx, self.eps, self.theta_global, self.theta_local, self.swa_period, self.window,
-                             capi.GG_ATTN_GEMMA3 if self.window else capi.GG_ATTN_REFERENCE)
+                             capi.GG_ATTN_GEMMA3 if self.window else capi.GG_ATTN_REFERENCE, prefill_batch)
 
     def weight_count(self) -> int:
         per_layer = self.hidden * (self.q_dim + 2 * self.kv_dim) + self.q_dim * self.hidden + 3 * self.hidden * self.inter
