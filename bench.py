@@ -80,6 +80,35 @@ def prefill_flops(shape, m: int) -> float:
     return gemm + attn
 
 
+def copy_calibration(nbytes: int):
+    """One device-to-device copy of nbytes (the runtime's copy kernel): the
+    reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to
+    HBM bytes."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), ctypes.c_size_t(nbytes)) or hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(nbytes)):
+        raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(a, 1, ctypes.c_size_t(nbytes))
+    hip.hipMemcpy(b, a, ctypes.c_size_t(nbytes), 3)   # hipMemcpyDeviceToDevice
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by the copy calibration)."""
+    path = os.path.join(ROOT, "profiles", "gate_up_gemv_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split()[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(shape, tensors, pos0: int, budget_s: float, threads: int):
     from oracle import oracle as orc
     orc.set_threads(threads)
@@ -111,6 +140,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--reference-mode", action="store_true", help="full attention, one theta (src/ as shipped)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="run one device-to-device copy of BYTES first (PMC calibration runs)")
     ap.add_argument("--token-prefill", action="store_true",
                     help="fill the context token by token (the reference's prefillBatched) instead of batched")
     args = ap.parse_args()
@@ -119,6 +150,8 @@ def main():
               f"runs on a single MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
     ctx_len = max(4096, args.ctx + args.warmup + args.steps + 8)
     shape = synth.GEMMA3_1B.with_ctx(ctx_len)
     shape = shape.reference_mode() if args.reference_mode else shape.gemma3_mode()
@@ -188,7 +221,7 @@ def main():
                    "positions": [pos_timed0, pos - 1]},
         "roofline": {"bound": "hbm", "kernel": f"{args.probe} GEMV (layer {args.probe_layer})",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": k_bytes, "avg_launch_us": round(k_ms * 1e3, 2)},
         "step_roofline": {"bytes_per_token": int(avg_bytes),
                           "achieved_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),

@@ -61,18 +61,26 @@ def test_gemv_repack_preserves_bytes(gpu, k, n):
     w = empty(capi.q8_0_packed_size(n, k))
     capi.q8_0_repack(src.data_ptr(), w.data_ptr(), n, k, stream())
     packed = host(w, np.uint8)
-    # pair (row r, col c) at ((g * KpS + c // CI) * 64 + (c % CI) * GR + r % GR) * 68
+    # item-planar layout: pair (row r, col c) is slot (c % CI) * GR + r % GR of
+    # item (r // GR) * KpS + c // CI (4352 bytes each); dword j of slot s sits
+    # at 1024 (j // 4) + 16 s + 4 (j % 4) for j < 16 and at 4096 + 4 s for j = 16
     kp = k // 64
     gr = 64 if n >= 8192 else 8
     ci = 64 // gr
     kps = -(-kp // ci)
-    assert packed.nbytes == n // gr * kps * 64 * 68
+    assert packed.nbytes == n // gr * kps * 4352
     pairs = blocks.reshape(n, kp, 68)
     rng = np.random.default_rng(0)
+
+    def pair_at(r, c):
+        item = (r // gr * kps + c // ci) * 4352
+        slot = (c % ci) * gr + r % gr
+        offs = [item + (1024 * (j // 4) + 16 * slot + 4 * (j % 4) if j < 16 else 4096 + 4 * slot) for j in range(17)]
+        return np.concatenate([packed[o:o + 4] for o in offs])
+
     for r, c in [(0, 0), (63, kp - 1), (64, 0), (n - 1, kp - 1)] + [(int(a), int(b)) for a, b in
                                                                     zip(rng.integers(0, n, 50), rng.integers(0, kp, 50))]:
-        off = ((r // gr * kps + c // ci) * 64 + (c % ci) * gr + r % gr) * 68
-        assert np.array_equal(packed[off:off + 68], pairs[r, c])
+        assert np.array_equal(pair_at(r, c), pairs[r, c])
     # every GGUF byte appears exactly once: total of all pairs equals the input bytes
     used = n * kp * 68
     assert used == blocks.nbytes

@@ -1,21 +1,24 @@
 // gg_internal.h -- argument blocks shared by the gfx950 kernels
 // (gg_kernels.hip) and the runtime that launches them (gg_runtime.hip).
 //
-// Device weight layout ("pair-interleaved Q8_0"). A Q8_0 weight matrix with
-// N output rows and K inputs keeps the GGUF 34-byte blocks verbatim (f16 LE
-// scale + 32 int8) but orders them so that one wavefront load is 4352
-// contiguous bytes:
-//   * two consecutive blocks of a row form a 68-byte "pair" (64 weights);
-//     Kp = K / 64 pairs per row;
+// Device weight layout ("item-planar Q8_0"). A Q8_0 weight matrix with N
+// output rows and K inputs keeps the bytes of the GGUF 34-byte blocks (f16 LE
+// scale + 32 int8) but orders them so that one wavefront reads 4352
+// contiguous bytes with fully coalesced 16-byte loads:
+//   * two consecutive blocks of a row form a 68-byte "pair" (64 weights,
+//     17 dwords); Kp = K / 64 pairs per row;
 //   * rows are grouped GR at a time and pair-columns CI at a time, GR * CI =
-//     64 (one pair per lane of a wavefront); a lane l of a wave holds row
-//     l % GR and pair-column offset l / GR of the current column step;
-//   * pair (row r, pair-column c) lives at byte
-//       ((g * KpS + c / CI) * 64 + (c % CI) * GR + r % GR) * 68,
-//     g = r / GR, KpS = ceil(Kp / CI) column steps per row group.
-// When CI does not divide Kp the last step of each group has unused slots;
-// they are allocated but never read. Every lane's 68 bytes start on a 4-byte
-// boundary, and the bytes read per token are exactly the GGUF count.
+//     64 pairs per "item"; slot s = (c % CI) * GR + r % GR of item
+//     g * KpS + c / CI holds pair (row r, pair-column c), g = r / GR,
+//     KpS = ceil(Kp / CI) items per row group; items are 4352 bytes apart;
+//   * inside an item the 64 pairs are stored as planes: dwords 4j..4j+3 of
+//     slot s at byte 1024 j + 16 s (j < 4) and dword 16 at 4096 + 4 s, so
+//     lane s of a wave loads its pair with four dwordx4 loads that each
+//     cover 1024 contiguous bytes, plus one dword load.
+// When CI does not divide Kp the last item of each group has unused slots;
+// they are allocated but hold no weights. Bytes read per token are the GGUF
+// count plus those slots (none for the Gemma-3 1B shapes but K = 1152 with
+// CI = 8, where a third of the last item of each group is padding).
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -31,7 +34,12 @@ constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
 constexpr int kAttnChunk = 32;       // base positions per attention block (4 waves x 8)
 constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per token
 
-// Q8_0 matrix in the pair-interleaved layout.
+// Byte offset of dword j (0..16) of slot s (0..63) inside a 4352-byte item.
+inline constexpr int plane_offset(int j, int s) {
+  return j < 16 ? 1024 * (j >> 2) + 16 * s + 4 * (j & 3) : 4096 + 4 * s;
+}
+
+// Q8_0 matrix in the item-planar layout.
 struct Q8Layout {
   int rows, K, Kp, CI, GR, KpS;
   size_t bytes() const { return (size_t)(rows / GR) * KpS * kColBytes; }

@@ -75,32 +75,63 @@ __device__ __forceinline__ float block_max256(float v, float* sh4) {
   return fmaxf(fmaxf(sh4[0], sh4[1]), fmaxf(sh4[2], sh4[3]));
 }
 
+// Full-wave sum on the DPP network (no LDS round trips), the total
+// broadcast through lane 63: pairs, quads, half rows, rows, then the
+// row_bcast15 / row_bcast31 steps that fold rows 0-2 into row 3.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  x += dpp_mov<0xB1>(x);         // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4E>(x);         // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);        // row_half_mirror
+  x += dpp_mov<0x140>(x);        // row_mirror
+  x += dpp_mov<0x142, 0xa>(x);   // row_bcast15 into rows 1 and 3
+  x += dpp_mov<0x143, 0xc>(x);   // row_bcast31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
 // One 68-byte pair = blocks 2c and 2c+1 of a row: 17 dwords.
 struct Pair {
   uint32_t w[17];
 };
 
-__device__ __forceinline__ void load_pair(const uint8_t* p, Pair& P) {
-  const u32x4a4 a = *(const u32x4a4*)(p);
-  const u32x4a4 b = *(const u32x4a4*)(p + 16);
-  const u32x4a4 c = *(const u32x4a4*)(p + 32);
-  const u32x4a4 d = *(const u32x4a4*)(p + 48);
+// Lane `lane` of a wave loads slot `lane` of a 4352-byte item (item-planar
+// layout): four dwordx4 loads over 1024 contiguous bytes each, one dword load.
+__device__ __forceinline__ void load_planes(const uint8_t* item, int lane, Pair& P) {
+  const uint4* p4 = (const uint4*)item;
+  const uint4 a = p4[lane], b = p4[64 + lane], c = p4[128 + lane], d = p4[192 + lane];
   P.w[0] = a.x; P.w[1] = a.y; P.w[2] = a.z; P.w[3] = a.w;
   P.w[4] = b.x; P.w[5] = b.y; P.w[6] = b.z; P.w[7] = b.w;
   P.w[8] = c.x; P.w[9] = c.y; P.w[10] = c.z; P.w[11] = c.w;
   P.w[12] = d.x; P.w[13] = d.y; P.w[14] = d.z; P.w[15] = d.w;
-  P.w[16] = *(const uint32_t*)(p + 64);
+  P.w[16] = ((const uint32_t*)(item + 4096))[lane];
 }
 
 // acc += (sum_j q0[j] x[j]) * d0 + (sum_j q1[j] x[32+j]) * d1, each block sum
-// running over j in order like linearQ8 (shaders.ts:123-142).
-// Pair bytes: [0,2) d0 | [2,34) q0 | [34,36) d1 | [36,68) q1.
+// running over j in order like linearQ8 (shaders.ts:123-142). xc is 16-byte
+// aligned (LDS). Pair bytes: [0,2) d0 | [2,34) q0 | [34,36) d1 | [36,68) q1.
 __device__ __forceinline__ float dot_pair(const Pair& P, const float* __restrict__ xc, float acc) {
+  const float4* x4 = (const float4*)xc;
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) s0 = fmaf(sbyte(P.w[(2 + j) >> 2], (2 + j) & 3), xc[j], s0);
+  for (int j4 = 0; j4 < 8; ++j4) {
+    const float4 xv = x4[j4];
+    const int j = 4 * j4;
+    s0 = fmaf(sbyte(P.w[(2 + j) >> 2], (2 + j) & 3), xv.x, s0);
+    s0 = fmaf(sbyte(P.w[(3 + j) >> 2], (3 + j) & 3), xv.y, s0);
+    s0 = fmaf(sbyte(P.w[(4 + j) >> 2], (4 + j) & 3), xv.z, s0);
+    s0 = fmaf(sbyte(P.w[(5 + j) >> 2], (5 + j) & 3), xv.w, s0);
+  }
 #pragma unroll
-  for (int j = 0; j < 32; ++j) s1 = fmaf(sbyte(P.w[9 + (j >> 2)], j & 3), xc[32 + j], s1);
+  for (int j4 = 0; j4 < 8; ++j4) {
+    const float4 xv = x4[8 + j4];
+    s1 = fmaf(sbyte(P.w[9 + j4], 0), xv.x, s1);
+    s1 = fmaf(sbyte(P.w[9 + j4], 1), xv.y, s1);
+    s1 = fmaf(sbyte(P.w[9 + j4], 2), xv.z, s1);
+    s1 = fmaf(sbyte(P.w[9 + j4], 3), xv.w, s1);
+  }
   acc = fmaf(s0, f16_lo(P.w[0]), acc);
   acc = fmaf(s1, f16_hi(P.w[8]), acc);
   return acc;
@@ -126,11 +157,13 @@ __device__ __forceinline__ float embed_elem(const GemvArgs& a, int token, int e)
   // tied embedding (layout with CI = 1, GR = 64).
   const int g = token >> 6, ln = token & 63;
   const int b = e >> 5, c = b >> 1;
-  const uint8_t* pr = a.embd + (((size_t)g * a.embd_KpS + c) * 64 + ln) * kPairBytes;
+  const uint8_t* item = a.embd + ((size_t)g * a.embd_KpS + c) * kColBytes;
+  // byte o of the pair: dword o / 4 of slot ln, byte o % 4
+  auto pb = [&](int o) { return item[plane_offset(o >> 2, ln) + (o & 3)]; };
   const int off = (b & 1) ? 34 : 0;
-  const uint16_t sb = (uint16_t)(pr[off] | (pr[off + 1] << 8));
+  const uint16_t sb = (uint16_t)(pb(off) | (pb(off + 1) << 8));
   const float scale = (float)__builtin_bit_cast(_Float16, sb);
-  const float q = (float)(int8_t)pr[off + 2 + (e & 31)];
+  const float q = (float)(int8_t)pb(off + 2 + (e & 31));
   const float t = q * scale;
   return t * a.embed_scale;
 }
@@ -205,30 +238,31 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 dequant-GEMV. Block = 256 threads = 4 wavefronts on one group of GR
-// rows; lane l holds row l % GR and pair-column phase l / GR. Wave w takes
-// column steps w, w+4, ...; each step is one 4352-byte contiguous load per
-// wave. Up to kStepsInFlight steps per wave are issued at kernel entry,
-// before the prologue (weights never depend on x), so a launch costs about
-// one memory latency; longer rows continue with a two-step prefetch.
+// Q8_0 dequant-GEMV, one row group per block (used with CI = 1: the tied LM
+// head, 64 rows per block). Block = 256 threads = 4 wavefronts on one group
+// of GR rows; lane l holds slot l of each item (row l % GR, pair-column phase
+// l / GR). Wave w takes items w, w+4, ... of the group. Up to kStepsInFlight
+// items per wave are issued at kernel entry, before the prologue (weights
+// never depend on x); longer rows continue with a two-item prefetch.
 // ---------------------------------------------------------------------------
 template <int PRO, int EPI, int CI, int kStepsInFlight>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   constexpr int GR = 64 / CI;
-  extern __shared__ float xs[];
+  extern __shared__ float4 xs4[];
+  float* xs = (float*)xs4;
   __shared__ float red[4][GR];
   __shared__ float sh4[4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = blockIdx.x;
   const int cp = lane / GR;
   const int Kp = a.Kp, KpS = a.KpS;
-  const uint8_t* base = a.W + ((size_t)g * KpS * 64 + lane) * kPairBytes;
+  const uint8_t* base = a.W + (size_t)g * KpS * kColBytes;
 
   Pair st[kStepsInFlight];
 #pragma unroll
   for (int i = 0; i < kStepsInFlight; ++i) {
     const int s = wv + 4 * i;
-    if (s < KpS && s * CI + cp < Kp) load_pair(base + (size_t)s * kColBytes, st[i]);
+    if (s < KpS && s * CI + cp < Kp) load_planes(base + (size_t)s * kColBytes, lane, st[i]);
   }
 
   gemv_prologue<PRO>(a, xs, Kp * 64, sh4);
@@ -244,12 +278,12 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   int s = wv + 4 * kStepsInFlight;
   if (s < KpS) {
     Pair cur, nxt;
-    if (s * CI + cp < Kp) load_pair(base + (size_t)s * kColBytes, cur);
-    if (s + 4 < KpS && (s + 4) * CI + cp < Kp) load_pair(base + (size_t)(s + 4) * kColBytes, nxt);
+    if (s * CI + cp < Kp) load_planes(base + (size_t)s * kColBytes, lane, cur);
+    if (s + 4 < KpS && (s + 4) * CI + cp < Kp) load_planes(base + (size_t)(s + 4) * kColBytes, lane, nxt);
     for (; s < KpS; s += 4) {
       Pair nn;
       const int s3 = s + 8;
-      if (s3 < KpS && s3 * CI + cp < Kp) load_pair(base + (size_t)s3 * kColBytes, nn);
+      if (s3 < KpS && s3 * CI + cp < Kp) load_planes(base + (size_t)s3 * kColBytes, lane, nn);
       const int c = s * CI + cp;
       if (c < Kp) acc = dot_pair(cur, xs + c * kXPad, acc);
       cur = nxt;
@@ -269,6 +303,167 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     // gate rows g*GR/2 + i sit in lanes 0..GR/2-1, the matching up rows in GR/2..GR-1
     const float up = __shfl(r, lane + GR / 2, 64);
     if (lane < GR / 2) a.act_out[g * (GR / 2) + lane] = gelu_mul(r, up);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 dequant-GEMV over balanced ranges of row groups (used with CI = 8: QKV,
+// O, gate/up, down). Block b owns groups [b G / nb, (b+1) G / nb); their
+// items (memory-contiguous, KpS per group) are split evenly over the W
+// waves. Every load is issued unconditionally (indices clamped into range)
+// so the wait counters stay exact: the prologue's vector loads go first, then
+// all NIF weight items of the wave, and the prologue only waits for its own
+// loads. Dot products accumulate per lane while a wave stays in one group;
+// one butterfly over the CI column phases per group lands the row sums in
+// the wave's LDS slots, and a fixed-order sum over the waves gives the rows
+// (deterministic). Prologue reductions run on the DPP network.
+// ---------------------------------------------------------------------------
+constexpr int kMgRows = 256;   // rows one block may own
+template <int PRO, int EPI, int W, int NIF, int EPT>
+__global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
+  constexpr int CI = 8, GR = 8;
+  constexpr int NT = 64 * W;
+  extern __shared__ float4 xs4[];
+  float* xs = (float*)xs4;
+  __shared__ float red[W][kMgRows];
+  __shared__ float shw[2][W];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int cp = lane / GR;
+  const int Kp = a.Kp, KpS = a.KpS, K = Kp * 64;
+  const int G = a.N / GR;
+  const int b = blockIdx.x, nb = gridDim.x;
+  const int g0 = (int)(((long long)b * G) / nb), g1 = (int)(((long long)(b + 1) * G) / nb);
+  const int i0 = g0 * KpS, ni = (g1 - g0) * KpS;
+  const int wi0 = i0 + (wv * ni) / W, wi1 = i0 + ((wv + 1) * ni) / W;
+  const int n = (K - tid + NT - 1) / NT;   // x elements this thread owns
+
+  // 1. prologue loads (clamped indices: always issued)
+  float v[EPT], res[EPT], wq[EPT], wp[EPT];
+  if (PRO == PRO_EMBED_NORM) {
+    const int token = a.tokens[a.st->cursor];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = min(tid + NT * i, K - 1);
+      v[i] = embed_elem(a, token, e);
+      wp[i] = a.w_pre[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = min(tid + NT * i, K - 1);
+      if (PRO == PRO_NONE) {
+        v[i] = a.x[e];
+      } else {
+        v[i] = a.pre_vec[e];
+        res[i] = a.pre_res[e];
+        wq[i] = a.w_post[e];
+        wp[i] = a.w_pre[e];
+      }
+    }
+  }
+  // 2. this wave's weight items (clamped into the block's range)
+  Pair st[NIF];
+#pragma unroll
+  for (int k = 0; k < NIF; ++k) {
+    const int it = max(min(wi0 + k, wi1 - 1), i0);
+    load_planes(a.W + (size_t)it * kColBytes, lane, st[k]);
+  }
+  for (int i = tid; i < W * kMgRows; i += NT) (&red[0][0])[i] = 0.f;
+
+  // 3. prologue -> x in LDS
+  if (PRO == PRO_NONE) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+      if (i < n) xs[xs_index(tid + NT * i)] = v[i];
+  } else {
+    float r[EPT];
+    if (PRO == PRO_EMBED_NORM) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) r[i] = v[i];
+    } else {   // res = pre_res + norm(pre_vec) * w_post (fusedNormAdd, shaders.ts:415)
+      float s1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i)
+        if (i < n) s1 = fmaf(v[i], v[i], s1);
+      s1 = wave_sum_dpp(s1);
+      if (lane == 0) shw[0][wv] = s1;
+      __syncthreads();
+      float t1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) t1 += shw[0][w];
+      const float rms1 = sqrtf(t1 / (float)K + a.eps);
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) r[i] = res[i] + (v[i] * wq[i]) / rms1;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+      if (i < n) ss = fmaf(r[i], r[i], ss);
+    if (b == 0) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i)
+        if (i < n) {
+          a.res_out[tid + NT * i] = r[i];
+          if (PRO == PRO_RESID_NORM && a.hist_out) a.hist_out[tid + NT * i] = r[i];
+        }
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) shw[1][wv] = ss;
+    __syncthreads();
+    float t2 = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t2 += shw[1][w];
+    const float rms = sqrtf(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+      if (i < n) xs[xs_index(tid + NT * i)] = (r[i] * wp[i]) / rms;
+  }
+  __syncthreads();
+
+  // 4. dot products in item order
+  float acc = 0.f;
+  int gcur = wi0 / KpS - g0;
+  auto flush = [&](int gl) {
+    float t = acc;
+#pragma unroll
+    for (int m = GR; m < 64; m <<= 1) t += __shfl_xor(t, m, 64);
+    if (lane < GR) red[wv][gl * GR + lane] = t;
+  };
+#pragma unroll
+  for (int k = 0; k < NIF; ++k) {
+    const int it = wi0 + k;
+    const int g = it / KpS, s = it - g * KpS;
+    const int c = s * CI + cp;
+    float d = dot_pair(st[k], xs + min(c, Kp - 1) * kXPad, 0.f);
+    d = (c < Kp && it < wi1) ? d : 0.f;
+    if (it < wi1 && g - g0 != gcur) {
+      flush(gcur);
+      gcur = g - g0;
+      acc = 0.f;
+    }
+    acc += d;
+  }
+  if (wi1 > wi0) flush(gcur);
+  __syncthreads();
+
+  // 5. fixed-order sum over the waves; epilogue
+  const int nrows = (g1 - g0) * GR;
+  for (int t = tid; t < nrows; t += NT) {
+    float r = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) r += red[w][t];
+    if (EPI == EPI_OUT) {
+      a.out[g0 * GR + t] = r;
+    } else {
+      // gate rows of a group in its first GR/2 slots, the matching up rows next
+      const int rr = t % GR;
+      if (rr < GR / 2) {
+        float up = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) up += red[w][t + GR / 2];
+        a.act_out[(g0 * GR + t - rr) / 2 + rr] = gelu_mul(r, up);
+      }
+    }
   }
 }
 
@@ -848,8 +1043,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   const int ar = tid >> 2, ak = (tid & 3) * 16;
   const float* arow = a.A + (size_t)min(m0 + ar, a.M - 1) * a.K + ak;
   const int wn_row = n0 + (tid & 127);
-  const uint8_t* wbase = a.W + (((size_t)(wn_row >> 3) * a.KpS) * 64 + (wn_row & 7)) * kPairBytes;
-  auto wpair = [&](int c) { return wbase + ((size_t)(c >> 3) * 64 + (c & 7) * 8) * kPairBytes; };
+  // pair (row wn_row, column c): item (wn_row / 8) * KpS + c / 8, slot (c % 8) * 8 + wn_row % 8
+  const uint8_t* wbase = a.W + (size_t)(wn_row >> 3) * a.KpS * kColBytes;
+  auto wload = [&](int c, Pair& P) { load_planes(wbase + (size_t)(c >> 3) * kColBytes, (c & 7) * 8 + (wn_row & 7), P); };
 
   f32x4 acc[2][4];
 #pragma unroll
@@ -861,7 +1057,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   Pair wp;
 #pragma unroll
   for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + 4 * q);
-  if (tid < 128) load_pair(wpair(0), wp);
+  if (tid < 128) wload(0, wp);
 
   for (int c = 0; c < a.Kp; ++c) {
 #pragma unroll
@@ -888,7 +1084,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     if (c + 1 < a.Kp) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + (size_t)(c + 1) * 64 + 4 * q);
-      if (tid < 128) load_pair(wpair(c + 1), wp);
+      if (tid < 128) wload(c + 1, wp);
     }
 #pragma unroll
     for (int kk = 0; kk < 64; kk += 4) {
@@ -1008,7 +1204,7 @@ __global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
 // ---------------------------------------------------------------------------
 // Upload helpers.
 // k_repack: GGUF row-major Q8_0 (rows of Kp 68-byte pairs) -> the
-// pair-interleaved layout L. interleave_half > 0 places source row r at fused
+// item-planar layout L. interleave_half > 0 places source row r at fused
 // row (r / half) * GR + (r % half) + dst_row_offset with half = GR / 2, i.e.
 // gate rows in the first half of each row group and (dst_row_offset = half)
 // the matching up rows in the second half.
@@ -1024,9 +1220,10 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t* __restrict__ src,
   const long long g = R / L.GR;
   const int ln = (int)(R - g * L.GR);
   const uint32_t* s = (const uint32_t*)(src + (size_t)idx * kPairBytes);
-  uint32_t* d = (uint32_t*)(dst + (((size_t)g * L.KpS + c / L.CI) * 64 + (c % L.CI) * L.GR + ln) * kPairBytes);
+  uint8_t* item = dst + ((size_t)g * L.KpS + c / L.CI) * kColBytes;
+  const int slot = (c % L.CI) * L.GR + ln;
 #pragma unroll
-  for (int i = 0; i < 17; ++i) d[i] = s[i];
+  for (int i = 0; i < 17; ++i) *(uint32_t*)(item + plane_offset(i, slot)) = s[i];
 }
 
 // Bit-exact Q8_0 dequantisation of GGUF blocks (gguf.ts:107-124).
@@ -1078,16 +1275,71 @@ static int launch_gemv_ci(int ci, const GemvArgs& a, hipStream_t s) {
   return (int)hipErrorInvalidValue;
 }
 
+// Launch plan of k_gemv_mg: W = 4 waves for K <= 2048, 16 above; about two
+// blocks per CU (512 or 256 blocks, at most one per row group), more blocks
+// when a wave would otherwise hold more than three items in registers.
+// Returns false when no plan keeps every wave at <= 3 items.
+struct MgPlan { int W, nb, nif, ept; };
+static bool mg_plan(const GemvArgs& a, int pro, MgPlan& p) {
+  const int K = a.Kp * 64, G = a.N / 8;
+  p.W = K > 2048 ? 16 : 4;
+  if (pro != PRO_NONE && p.W != 4) return false;
+  const int ept = (K + 64 * p.W - 1) / (64 * p.W);
+  p.ept = ept <= 2 ? ept : ept <= 4 ? 4 : ept <= 5 ? 5 : 8;
+  int nb = min(G, p.W == 4 ? 512 : 256);
+  for (;;) {
+    const int gpb = (G + nb - 1) / nb;
+    const int nif = (gpb * a.KpS + p.W - 1) / p.W;
+    if (nif <= 3 && gpb * 8 <= kMgRows) {
+      p.nb = nb;
+      p.nif = nif;
+      return true;
+    }
+    if (nb == G) return false;
+    nb = min(G, nb * 2);
+  }
+}
+
+template <int PRO, int EPI, int W, int NIF>
+static int launch_mg_ept(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  const size_t lds = (size_t)a.Kp * kXPad * sizeof(float);
+  switch (p.ept) {
+#define GG_MG_EPT(E) \
+    case E: hipLaunchKernelGGL((k_gemv_mg<PRO, EPI, W, NIF, E>), dim3(p.nb), dim3(64 * W), lds, s, a); break;
+    GG_MG_EPT(1) GG_MG_EPT(2) GG_MG_EPT(4) GG_MG_EPT(5) GG_MG_EPT(8)
+#undef GG_MG_EPT
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+template <int PRO, int EPI, int W>
+static int launch_mg_nif(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  switch (p.nif) {
+    case 1: return launch_mg_ept<PRO, EPI, W, 1>(a, p, s);
+    case 2: return launch_mg_ept<PRO, EPI, W, 2>(a, p, s);
+    case 3: return launch_mg_ept<PRO, EPI, W, 3>(a, p, s);
+  }
+  return (int)hipErrorInvalidValue;
+}
+static int launch_mg(int pro, int epi, const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  if (pro == PRO_NONE) {
+    return p.W == 4 ? launch_mg_nif<PRO_NONE, EPI_OUT, 4>(a, p, s) : launch_mg_nif<PRO_NONE, EPI_OUT, 16>(a, p, s);
+  }
+  if (epi == EPI_GEGLU) return launch_mg_nif<PRO_RESID_NORM, EPI_GEGLU, 4>(a, p, s);
+  if (pro == PRO_EMBED_NORM) return launch_mg_nif<PRO_EMBED_NORM, EPI_OUT, 4>(a, p, s);
+  return launch_mg_nif<PRO_RESID_NORM, EPI_OUT, 4>(a, p, s);
+}
+
 int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a.Kp * 64 > kMaxK || a.Kp <= 0 || a.N <= 0 || (ci != 1 && ci != 8) || a.N % (64 / ci) ||
       a.KpS != (a.Kp + ci - 1) / ci)
     return (int)hipErrorInvalidValue;
   if (pro != PRO_NONE && a.Kp * 64 > kMaxEPT / 4 * 256) return (int)hipErrorInvalidValue;
-  if (epi == EPI_GEGLU) {
-    if (pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
-    return launch_gemv_ci<PRO_RESID_NORM, EPI_GEGLU>(ci, a, s);
-  }
+  if (epi == EPI_GEGLU && pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
+  MgPlan plan;
+  if (ci == 8 && mg_plan(a, pro, plan)) return launch_mg(pro, epi, a, plan, s);
+  if (epi == EPI_GEGLU) return launch_gemv_ci<PRO_RESID_NORM, EPI_GEGLU>(ci, a, s);
   if (pro == PRO_NONE) return launch_gemv_ci<PRO_NONE, EPI_OUT>(ci, a, s);
   if (pro == PRO_EMBED_NORM) return launch_gemv_ci<PRO_EMBED_NORM, EPI_OUT>(ci, a, s);
   if (pro == PRO_RESID_NORM) return launch_gemv_ci<PRO_RESID_NORM, EPI_OUT>(ci, a, s);
