@@ -32,7 +32,8 @@ constexpr int kColBytes = 64 * kPairBytes;   // one wavefront step: 4352 bytes
 constexpr int kMaxK = 8192;          // largest GEMV input (x staged in LDS)
 constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
 constexpr int kAttnChunk = 32;       // base positions per attention block (4 waves x 8)
-constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per token
+constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per query (batched prefill bound)
+constexpr int kDecMaxChunks = 64;    // decode attention chunks per token (16 while the span is <= 4096)
 
 // Byte offset of dword j (0..16) of slot s (0..63) inside a 4352-byte item.
 inline constexpr int plane_offset(int j, int s) {
@@ -76,7 +77,7 @@ struct DevState {
 };
 
 struct GemvArgs {
-  const uint8_t* W;     // pair-interleaved weights
+  const uint8_t* W;     // item-planar weights
   int Kp;               // pairs per row (K / 64)
   int KpS;              // column steps per row group
   int N;                // output rows
@@ -89,13 +90,18 @@ struct GemvArgs {
   const float* w_pre;      // pre-norm weight producing x
   float* res_out;          // block 0 writes the new residual stream vector here
   float* hist_out;         // optional second copy (per-layer hidden history)
-  const uint8_t* embd;     // pair-interleaved token embedding (EMBED_NORM)
+  const uint8_t* embd;     // item-planar token embedding (EMBED_NORM)
   int embd_KpS;            // its column steps per group (CI = 1)
   const DevState* st;
   const int32_t* tokens;
   float eps;
   float embed_scale;       // sqrtf((float)hidden)
   float* act_out;          // GEGLU epilogue output [N/2]
+  // PRO_ATTN_MERGE (attention output projection): x is the merge of the
+  // decode attention chunk partials of this token
+  const float* attn_part;  // o [kDecMaxChunks][kAttnMaxQ][256], then (m, l) [kDecMaxChunks][kAttnMaxQ][2]
+  int attn_window;         // the layer's sliding window (0: full causal)
+  float* x_out;            // block 0 stores the merged x here (the attention output)
 };
 
 struct AttnArgs {
@@ -110,17 +116,18 @@ struct AttnArgs {
   float eps;
   float scale;             // 1/sqrt(head_dim)
   const DevState* st;
-  float* part;             // [kAttnMaxChunks][n_q][2 + 256]
-  unsigned int* counter;   // arrivals of the chunk blocks (reset by the last)
+  float* part;             // decode: o [kDecMaxChunks][kAttnMaxQ][256] then (m, l) [kDecMaxChunks][kAttnMaxQ][2];
+                           // batched prefill: [row][kPrefillChunks][n_q][2 + 256]
+  unsigned int* counter;   // batched prefill: arrivals of a row's chunk blocks (reset by the last)
   float* attn_out;         // [n_q * 256]
   float* q_dbg;            // optional: normed+roped q of this token
   // batched prefill (k_attn<true>): query row r = blockIdx.y sits at position
   // pf_start + r; K/V of every prompt position are already in the cache
   int pf_start;
-  int max_chunks;          // chunk limit per query (kAttnMaxChunks for decode)
+  int max_chunks;          // batched prefill: chunks per query (kPrefillChunks)
 };
 
-// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W pair-interleaved (CI = 8).
+// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W item-planar (CI = 8).
 struct GemmArgs {
   const float* A;          // [M][K] row-major activations
   const uint8_t* W;
@@ -178,11 +185,13 @@ struct SelectArgs {
 };
 
 // ---- launchers (gg_kernels.hip) -------------------------------------------
-enum Prologue { PRO_NONE = 0, PRO_EMBED_NORM = 1, PRO_RESID_NORM = 2 };
+enum Prologue { PRO_NONE = 0, PRO_EMBED_NORM = 1, PRO_RESID_NORM = 2, PRO_ATTN_MERGE = 3 };
 enum Epilogue { EPI_OUT = 0, EPI_GEGLU = 1 };
 
 int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream);
 int launch_attention(const AttnArgs& a, int grid, void* stream);
+// decode attention grid for a context length: 16 chunks up to span 4096, else kDecMaxChunks
+inline int decode_attention_grid(int ctx) { return ctx <= 4096 ? 16 : kDecMaxChunks; }
 int launch_final(const FinalArgs& a, void* stream);
 int launch_select(const SelectArgs& a, void* stream);
 int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,

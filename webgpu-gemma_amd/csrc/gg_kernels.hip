@@ -92,6 +92,36 @@ __device__ __forceinline__ float wave_sum_dpp(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
+// DPP move whose rows outside ROWMASK read -inf (for max reductions).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_mov_ninf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
+                                                               __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
+}
+// Sum over each aligned group of 8 lanes, result in all 8 (quad_perm xor 1,
+// xor 2, then row_half_mirror pairs the two quads).
+__device__ __forceinline__ float group8_sum(float x) {
+  x += dpp_mov<0xB1>(x);
+  x += dpp_mov<0x4E>(x);
+  x += dpp_mov<0x141>(x);
+  return x;
+}
+// Sum / max over the whole wave of values that are uniform within each group
+// of 8 lanes: row_mirror pairs the two groups of a row, the row_bcast15 /
+// row_bcast31 steps fold rows 0-2 into row 3, lane 63 is broadcast.
+__device__ __forceinline__ float across8_sum(float x) {
+  x += dpp_mov<0x140>(x);
+  x += dpp_mov<0x142, 0xa>(x);
+  x += dpp_mov<0x143, 0xc>(x);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+__device__ __forceinline__ float across8_max(float x) {
+  x = fmaxf(x, dpp_mov<0x140>(x));
+  x = fmaxf(x, dpp_mov_ninf<0x142, 0xa>(x));
+  x = fmaxf(x, dpp_mov_ninf<0x143, 0xc>(x));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
 // One 68-byte pair = blocks 2c and 2c+1 of a row: 17 dwords.
 struct Pair {
   uint32_t w[17];
@@ -318,6 +348,18 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // the wave's LDS slots, and a fixed-order sum over the waves gives the rows
 // (deterministic). Prologue reductions run on the DPP network.
 // ---------------------------------------------------------------------------
+// Decode attention chunking (shared by k_attn_dec and the merge prologue).
+__device__ __forceinline__ void dec_span(int pos, int window, int* t_lo, int* ch, int* nch) {
+  const int lo = window > 0 ? max(0, pos - window + 1) : 0;
+  const int span = pos - lo + 1;
+  const int mc = span <= 4096 ? 16 : kDecMaxChunks;
+  const int c = kAttnChunk * ((span + kAttnChunk * mc - 1) / (kAttnChunk * mc));
+  *t_lo = lo;
+  *ch = c;
+  *nch = (span + c - 1) / c;
+}
+constexpr size_t kDecStatOff = (size_t)kDecMaxChunks * kAttnMaxQ * kHeadDim;   // (m, l) after the o block
+
 constexpr int kMgRows = 256;   // rows one block may own
 template <int PRO, int EPI, int W, int NIF, int EPT>
 __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
@@ -339,7 +381,24 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 
   // 1. prologue loads (clamped indices: always issued)
   float v[EPT], res[EPT], wq[EPT], wp[EPT];
-  if (PRO == PRO_EMBED_NORM) {
+  // PRO_ATTN_MERGE: thread t merges x[4t .. 4t+3] (head t / 64) from the
+  // first 16 chunk partials (more are merged in batches of 16 below)
+  constexpr int kMB = 16;
+  float am_m[kMB], am_l[kMB];
+  float4 am_o[kMB];
+  int nch = 0, ahd = 0;
+  if (PRO == PRO_ATTN_MERGE) {
+    int t_lo, ch;
+    dec_span(a.st->pos, a.attn_window, &t_lo, &ch, &nch);
+    ahd = min(tid >> 6, K / kHeadDim - 1);
+#pragma unroll
+    for (int k = 0; k < kMB; ++k) {
+      const int c = min(k, nch - 1);
+      am_m[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2];
+      am_l[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2 + 1];
+      am_o[k] = *(const float4*)(a.attn_part + ((size_t)c * kAttnMaxQ + ahd) * kHeadDim + 4 * (tid & 63));
+    }
+  } else if (PRO == PRO_EMBED_NORM) {
     const int token = a.tokens[a.st->cursor];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
@@ -375,6 +434,53 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
       if (i < n) xs[xs_index(tid + NT * i)] = v[i];
+  } else if (PRO == PRO_ATTN_MERGE) {
+    // chunk weights exp(m_c - M) with M the running max, in chunk order
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMB; ++k)
+      if (k < nch) M = fmaxf(M, am_m[k]);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](int k, float Mx) {
+      const float f = expf(am_m[k] - Mx);
+      L = fmaf(f, am_l[k], L);
+      acc.x = fmaf(f, am_o[k].x, acc.x);
+      acc.y = fmaf(f, am_o[k].y, acc.y);
+      acc.z = fmaf(f, am_o[k].z, acc.z);
+      acc.w = fmaf(f, am_o[k].w, acc.w);
+    };
+#pragma unroll
+    for (int k = 0; k < kMB; ++k)
+      if (k < nch) add(k, M);
+    for (int c0 = kMB; c0 < nch; c0 += kMB) {   // spans above 4096 positions
+#pragma unroll
+      for (int k = 0; k < kMB; ++k) {
+        const int c = min(c0 + k, nch - 1);
+        am_m[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2];
+        am_l[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2 + 1];
+        am_o[k] = *(const float4*)(a.attn_part + ((size_t)c * kAttnMaxQ + ahd) * kHeadDim + 4 * (tid & 63));
+      }
+      float Mb = M;
+#pragma unroll
+      for (int k = 0; k < kMB; ++k)
+        if (c0 + k < nch) Mb = fmaxf(Mb, am_m[k]);
+      const float sc = expf(M - Mb);
+      L *= sc;
+      acc.x *= sc;
+      acc.y *= sc;
+      acc.z *= sc;
+      acc.w *= sc;
+      M = Mb;
+#pragma unroll
+      for (int k = 0; k < kMB; ++k)
+        if (c0 + k < nch) add(k, M);
+    }
+    if (4 * tid < K) {
+      const float4 xo = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+      *(float4*)&xs[xs_index(4 * tid)] = xo;
+      if (b == 0) *(float4*)(a.x_out + 4 * tid) = xo;
+    }
   } else {
     float r[EPT];
     if (PRO == PRO_EMBED_NORM) {
@@ -830,6 +936,223 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
   }
   for (int h = 0; h < nq; ++h) attn_out[h * kHeadDim + tid] = acc[h] / Lh[h];
   if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention (one KV head, head_dim 256, up to 4 query heads), one
+// chunk of positions per block; the chunk partials (max, sum, o) go to
+// memory and the attention output projection merges them in its prologue
+// (no cross-block step here). Chunks: 32 * ceil(span / (32 * mc)) positions,
+// mc = 16 while the span is <= 4096 (else kDecMaxChunks), so the merge reads
+// at most 16 partials per head at Gemma-3 1B lengths.
+//
+// Per block: QK-norm + NEOX RoPE of the query heads (wave h: head h) and, in
+// the block holding `pos`, of the key; that block also stores k/v to the
+// cache (fusedPerHeadNormRope + kvCacheStore, shaders.ts:209-227, 420-467).
+// Wave w then runs passes of 8 positions t0 + 32 p + 8 w + i: lane (i, o)
+// = (lane / 8, lane % 8) holds key dims 4 (o + 8 j) .. +3 (j < 8), so each
+// key load instruction reads 8 whole 128-byte segments, and the dot products
+// finish with a butterfly over the 8 lanes of a position; lane l holds value
+// dims 4 l .. 4 l + 3 for the weighted sum (shaders.ts:229-325). Softmax
+// statistics are kept online per pass; all reductions run on DPP (no LDS
+// round trips), probabilities reach every lane through readlane.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
+  constexpr int NQ = kAttnMaxQ;
+  __shared__ float4 qs4[NQ][64];
+  __shared__ float4 ks4[64], vs4[64];
+  __shared__ float4 wo[4][NQ][64];
+  __shared__ float wm[4][NQ], wl[4][NQ], fw[4][NQ];
+  __shared__ float hst[NQ][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nq = a.n_q;
+  const int nqd = nq * kHeadDim;
+  const int pos = a.st->pos;
+  int t_lo, ch, nch;
+  dec_span(pos, a.window, &t_lo, &ch, &nch);
+  const int b = blockIdx.x;
+  if (b >= nch) return;
+  const int t0 = t_lo + b * ch;
+  const int t1 = min(t0 + ch, pos + 1);
+  const int npass = (t1 - t0 + 31) >> 5;
+  const int kv_last = max(pos - 1, 0);     // cache rows [0, pos) hold earlier tokens
+  const int pl = lane >> 3, oc = lane & 7;
+  const bool holder = (b == nch - 1);      // this block's chunk contains pos
+
+  // loads of pass p: key rows in the score layout, value rows in the PV
+  // layout; rows are clamped into the cache (positions >= t1 are masked,
+  // pos itself is substituted from LDS)
+  float4 kr[8], vr[8];
+  auto load_k = [&](int p) {
+    const int t = min(t0 + 32 * p + 8 * wv + pl, kv_last);
+    const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kr[j] = kp[oc + 8 * j];
+  };
+  auto load_v = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = min(t0 + 32 * p + 8 * wv + i, kv_last);
+      vr[i] = *(const float4*)(a.v_cache + (size_t)t * kHeadDim + 4 * lane);
+    }
+  };
+  load_k(0);
+  load_v(0);
+  // the QKV output, norm weights and this position's RoPE row
+  const bool my_head = wv < nq;
+  float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hx[i] = a.qkv[min(wv, nq - 1) * kHeadDim + lane + 64 * i];
+    nwt[i] = a.q_norm[lane + 64 * i];
+    kx[i] = a.qkv[nqd + lane + 64 * i];
+    kwt[i] = a.k_norm[lane + 64 * i];
+  }
+  const float* rt = a.rope + (size_t)pos * kHeadDim;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cs[j] = rt[lane + 64 * j];
+    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
+  }
+  const float4 vme = *(const float4*)(a.qkv + nqd + kHeadDim + 4 * lane);
+
+  // RMSNorm + NEOX RoPE of one head: lane owns dims lane + 64 i; pairs (i, i + 128)
+  auto norm_rope = [&](float* x, const float* w, float* dst) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
+    ss = wave_sum_dpp(ss);
+    const float rms = sqrtf(ss / (float)kHeadDim + a.eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) / rms;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float x0 = x[j], x1 = x[j + 2];
+      dst[lane + 64 * j] = x0 * cs[j] - x1 * sn[j];
+      dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
+    }
+  };
+  if (my_head) norm_rope(hx, nwt, (float*)qs4[wv]);
+  else if (wv < NQ) qs4[wv][lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (holder && wv == 0) norm_rope(kx, kwt, (float*)ks4);
+  if (holder && wv == 1) vs4[lane] = vme;
+  __syncthreads();
+  if (holder) {
+    a.k_cache[(size_t)pos * kHeadDim + tid] = ((const float*)ks4)[tid];
+    a.v_cache[(size_t)pos * kHeadDim + tid] = ((const float*)vs4)[tid];
+  }
+  if (b == 0 && a.q_dbg)
+    for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = ((const float*)qs4[e >> 8])[e & 255];
+
+  float4 qr[NQ][8];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[h][j] = qs4[h][oc + 8 * j];
+
+  float m[NQ], l[NQ];
+  float4 o4[NQ];
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+    o4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int p = 0; p < npass; ++p) {
+    const int tb = t0 + 32 * p + 8 * wv;       // first position of this wave's pass
+    const int t = tb + pl;
+    if (t == pos) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kr[j] = ks4[oc + 8 * j];
+    }
+    float sc[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d = fmaf(qr[h][j].x, kr[j].x, d);
+        d = fmaf(qr[h][j].y, kr[j].y, d);
+        d = fmaf(qr[h][j].z, kr[j].z, d);
+        d = fmaf(qr[h][j].w, kr[j].w, d);
+      }
+      d = group8_sum(d);
+      sc[h] = (t < t1 && h < nq) ? d * a.scale : -INFINITY;
+    }
+    load_k(p + 1 < npass ? p + 1 : p);          // next pass (a repeat on the last)
+    float pr[NQ], alpha[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      const float mx = across8_max(sc[h]);
+      const float mn = fmaxf(m[h], mx);
+      alpha[h] = (m[h] == -INFINITY) ? 0.f : expf(m[h] - mn);
+      pr[h] = (sc[h] == -INFINITY) ? 0.f : expf(sc[h] - mn);
+      l[h] = fmaf(l[h], alpha[h], across8_sum(pr[h]));
+      m[h] = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (tb + i == pos) vr[i] = vs4[lane];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+      o4[h].x *= alpha[h];
+      o4[h].y *= alpha[h];
+      o4[h].z *= alpha[h];
+      o4[h].w *= alpha[h];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[h]), 8 * i));
+        o4[h].x = fmaf(pv, vr[i].x, o4[h].x);
+        o4[h].y = fmaf(pv, vr[i].y, o4[h].y);
+        o4[h].z = fmaf(pv, vr[i].z, o4[h].z);
+        o4[h].w = fmaf(pv, vr[i].w, o4[h].w);
+      }
+    }
+    load_v(p + 1 < npass ? p + 1 : p);
+  }
+
+  // merge the four waves (fixed order) into the chunk's (max, sum, o)
+#pragma unroll
+  for (int h = 0; h < NQ; ++h) wo[wv][h][lane] = o4[h];
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) { wm[wv][h] = m[h]; wl[wv][h] = l[h]; }
+  }
+  __syncthreads();
+  if (tid < NQ) {
+    const int h = tid;
+    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
+      fw[w][h] = f;
+      L = fmaf(f, wl[w][h], L);
+    }
+    hst[h][0] = M;
+    hst[h][1] = L;
+  }
+  __syncthreads();
+  const int h = tid >> 6, q = tid & 63;       // thread: head h, dims 4 q .. 4 q + 3
+  if (h < nq) {
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = fw[w][h];
+      const float4 v = wo[w][h][q];
+      O.x = fmaf(f, v.x, O.x);
+      O.y = fmaf(f, v.y, O.y);
+      O.z = fmaf(f, v.z, O.z);
+      O.w = fmaf(f, v.w, O.w);
+    }
+    *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * q) = O;
+    if (q == 0) {
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[h][0];
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[h][1];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1322,6 +1645,7 @@ static int launch_mg_nif(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
   return (int)hipErrorInvalidValue;
 }
 static int launch_mg(int pro, int epi, const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  if (pro == PRO_ATTN_MERGE) return launch_mg_nif<PRO_ATTN_MERGE, EPI_OUT, 4>(a, p, s);
   if (pro == PRO_NONE) {
     return p.W == 4 ? launch_mg_nif<PRO_NONE, EPI_OUT, 4>(a, p, s) : launch_mg_nif<PRO_NONE, EPI_OUT, 16>(a, p, s);
   }
@@ -1338,6 +1662,10 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
   if (pro != PRO_NONE && a.Kp * 64 > kMaxEPT / 4 * 256) return (int)hipErrorInvalidValue;
   if (epi == EPI_GEGLU && pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
   MgPlan plan;
+  if (pro == PRO_ATTN_MERGE) {   // only the multi-group kernel merges: K = n_q * 256 <= 1024 on 256 threads
+    if (ci != 8 || a.Kp * 64 > kAttnMaxQ * kHeadDim || a.Kp % 4 || !mg_plan(a, pro, plan)) return (int)hipErrorInvalidValue;
+    return launch_mg(pro, epi, a, plan, s);
+  }
   if (ci == 8 && mg_plan(a, pro, plan)) return launch_mg(pro, epi, a, plan, s);
   if (epi == EPI_GEGLU) return launch_gemv_ci<PRO_RESID_NORM, EPI_GEGLU>(ci, a, s);
   if (pro == PRO_NONE) return launch_gemv_ci<PRO_NONE, EPI_OUT>(ci, a, s);
@@ -1347,9 +1675,8 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
 }
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
-  if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kAttnMaxChunks || a.max_chunks != kAttnMaxChunks)
-    return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kDecMaxChunks) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_dec, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

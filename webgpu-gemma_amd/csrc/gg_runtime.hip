@@ -243,20 +243,22 @@ int record_forward(gg_ctx* c) {
     at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
     at.st = c->st;
     at.part = c->attn_part;
-    at.counter = c->counters;
     at.attn_out = c->attn_out;
-    at.max_chunks = kAttnMaxChunks;
+    at.max_chunks = kDecMaxChunks;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
       ProbeScope ps(c, GG_PROBE_ATTN, l);
       GG_TRY(launch_rc(c, launch_attention(at, c->attn_grid, c->stream), "attention"));
     }
-    // O projection
+    // O projection; its prologue merges the attention chunks into attn_out
     GemvArgs o = gemv_base(Ly.o, c->lay_o, c->o_out);
-    o.x = c->attn_out;
+    o.attn_part = c->attn_part;
+    o.attn_window = at.window;
+    o.x_out = c->attn_out;
+    o.st = c->st;
     {
       ProbeScope ps(c, GG_PROBE_O, l);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_o.CI, o, c->stream), "o gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(PRO_ATTN_MERGE, EPI_OUT, c->lay_o.CI, o, c->stream), "o gemv"));
     }
     // gate/up with post-attn norm + residual + ffn_norm, GeGLU epilogue
     GemvArgs gu = gemv_base(Ly.gu, c->lay_gu, nullptr);
@@ -639,7 +641,7 @@ int gg_finalize(gg_ctx* c) {
       return set_err(c, GG_ERR_MISSING, "missing tensors of blk." + std::to_string(l));
   if (c->staging) { (void)hipFree(c->staging); c->staging = nullptr; c->staging_bytes = 0; }
 
-  c->attn_grid = std::min(kAttnMaxChunks, cdiv(c->CTX, kAttnChunk));
+  c->attn_grid = decode_attention_grid(c->CTX);
 
   const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
   for (Layer& Ly : c->layers) {
@@ -649,8 +651,8 @@ int gg_finalize(gg_ctx* c) {
     GG_HIP(c, hipMemset(Ly.vc, 0, kvb));
   }
   GG_TRY(dalloc(c, &c->qkv_out, (size_t)c->NQKV * 4));
-  // sized for kAttnMaxQ heads: the merge reads whole head slots of a chunk
-  GG_TRY(dalloc(c, &c->attn_part, (size_t)kAttnMaxChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
+  // decode chunk partials: o [kDecMaxChunks][kAttnMaxQ][256], then (m, l)
+  GG_TRY(dalloc(c, &c->attn_part, (size_t)kDecMaxChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
   GG_TRY(dalloc(c, &c->attn_out, (size_t)c->QD * 4));
   GG_TRY(dalloc(c, &c->o_out, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->act, (size_t)c->I * 4));
