@@ -149,6 +149,10 @@ int gg_last_timing(gg_ctx* ctx, float* forward_ms, float* select_ms);
 #define GG_PROBE_SELECT 7    /* vocab selector                            */
 int gg_set_probe(gg_ctx* ctx, int32_t kind, int32_t layer);
 int gg_probe_elapsed(gg_ctx* ctx, float* ms);
+/* Device time between two event-record nodes placed back to back right
+ * before the probed launch (same graph, same step): the cost of an event
+ * bracket itself, to subtract from gg_probe_elapsed. */
+int gg_probe_overhead(gg_ctx* ctx, float* ms);
 
 /* Message for the last failing call on ctx (or of gg_create when ctx is NULL). */
 const char* gg_last_error(const gg_ctx* ctx);
@@ -160,7 +164,7 @@ void gg_destroy(gg_ctx* ctx);
  * These expose single kernels of the path for isolated parity tests and the
  * GEMV benchmark; `stream` is a hipStream_t (NULL = default stream). */
 
-/* Device bytes of the pair-interleaved layout of a rows x k Q8_0 matrix
+/* Device bytes of the item-planar layout of a rows x k Q8_0 matrix
  * (>= the GGUF count rows*k/32*34; 0 for unsupported shapes: rows and k must
  * be multiples of 64, k <= 8192). */
 size_t gg_q8_0_packed_size(int64_t rows, int64_t k);

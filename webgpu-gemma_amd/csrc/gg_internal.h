@@ -48,7 +48,11 @@ struct Q8Layout {
 
 // The layout of a matrix: whole 64-row groups (CI = 1) for tall matrices,
 // 8-row groups with 8 pair-columns per step (CI = 8) below 8192 rows, so that
-// even N = 1152 gets 144 blocks without splitting K.
+// even N = 1152 gets 144 blocks without splitting K. force_ci = 2 (32-row
+// groups) leaves no padding when Kp is even but not a multiple of 8.
+// CI without padding for a row of Kp pair-columns: 8 when it divides Kp, else 2.
+inline int padfree_ci(int Kp) { return (Kp % 8 == 0 || Kp % 2) ? 8 : 2; }
+
 inline Q8Layout q8_layout(int rows, int K, int force_ci = 0) {
   Q8Layout L;
   L.rows = rows;
@@ -127,11 +131,11 @@ struct AttnArgs {
   int max_chunks;          // batched prefill: chunks per query (kPrefillChunks)
 };
 
-// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W item-planar (CI = 8).
+// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W item-planar (GR = 8 or 32).
 struct GemmArgs {
   const float* A;          // [M][K] row-major activations
   const uint8_t* W;
-  int M, N, K, Kp, KpS;
+  int M, N, K, Kp, KpS, GR;
   float* C;                // [M][N] (EPI_OUT) or act [M][N/2] (EPI_GEGLU)
 };
 

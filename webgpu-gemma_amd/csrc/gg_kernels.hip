@@ -337,8 +337,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 dequant-GEMV over balanced ranges of row groups (used with CI = 8: QKV,
-// O, gate/up, down). Block b owns groups [b G / nb, (b+1) G / nb); their
+// Q8_0 dequant-GEMV over balanced ranges of row groups (used with CI = 8 or 2:
+// QKV, O, gate/up, down). Block b owns groups [b G / nb, (b+1) G / nb); their
 // items (memory-contiguous, KpS per group) are split evenly over the W
 // waves. Every load is issued unconditionally (indices clamped into range)
 // so the wait counters stay exact: the prologue's vector loads go first, then
@@ -361,9 +361,9 @@ __device__ __forceinline__ void dec_span(int pos, int window, int* t_lo, int* ch
 constexpr size_t kDecStatOff = (size_t)kDecMaxChunks * kAttnMaxQ * kHeadDim;   // (m, l) after the o block
 
 constexpr int kMgRows = 256;   // rows one block may own
-template <int PRO, int EPI, int W, int NIF, int EPT>
+template <int PRO, int EPI, int CI, int W, int NIF, int EPT>
 __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
-  constexpr int CI = 8, GR = 8;
+  constexpr int GR = 64 / CI;
   constexpr int NT = 64 * W;
   extern __shared__ float4 xs4[];
   float* xs = (float*)xs4;
@@ -1366,9 +1366,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   const int ar = tid >> 2, ak = (tid & 3) * 16;
   const float* arow = a.A + (size_t)min(m0 + ar, a.M - 1) * a.K + ak;
   const int wn_row = n0 + (tid & 127);
-  // pair (row wn_row, column c): item (wn_row / 8) * KpS + c / 8, slot (c % 8) * 8 + wn_row % 8
-  const uint8_t* wbase = a.W + (size_t)(wn_row >> 3) * a.KpS * kColBytes;
-  auto wload = [&](int c, Pair& P) { load_planes(wbase + (size_t)(c >> 3) * kColBytes, (c & 7) * 8 + (wn_row & 7), P); };
+  // pair (row wn_row, column c): item (wn_row / GR) * KpS + c / CI, slot (c % CI) * GR + wn_row % GR
+  const int GR = a.GR, CI = 64 / GR;
+  const uint8_t* wbase = a.W + (size_t)(wn_row / GR) * a.KpS * kColBytes;
+  auto wload = [&](int c, Pair& P) {
+    load_planes(wbase + (size_t)(c / CI) * kColBytes, (c % CI) * GR + wn_row % GR, P);
+  };
 
   f32x4 acc[2][4];
 #pragma unroll
@@ -1435,10 +1438,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         const float v = acc[i][j][r];
         if (EPI == EPI_OUT) {
           if (m < a.M) a.C[(size_t)m * a.N + n] = v;
-        } else {
+        } else if (a.GR == 8) {
           // fused gate/up rows: 4 gate rows then their 4 up rows per group of 8
           const float up = __shfl(v, lane + 4, 64);
           if (m < a.M && (n & 4) == 0) a.C[(size_t)m * (a.N / 2) + (n >> 3) * 4 + (n & 3)] = gelu_mul(v, up);
+        } else if ((j & 1) == 0) {
+          // groups of 32: 16 gate rows (tile j) then their 16 up rows (tile j + 1)
+          const float up = acc[i][(j + 1) & 3][r];
+          if (m < a.M) a.C[(size_t)m * (a.N / 2) + (n >> 5) * 16 + (n & 15)] = gelu_mul(v, up);
         }
       }
 }
@@ -1593,6 +1600,7 @@ template <int PRO, int EPI>
 static int launch_gemv_ci(int ci, const GemvArgs& a, hipStream_t s) {
   switch (ci) {
     case 1: return launch_gemv_nif<PRO, EPI, 1>(a, s);
+    case 2: return launch_gemv_nif<PRO, EPI, 2>(a, s);
     case 8: return launch_gemv_nif<PRO, EPI, 8>(a, s);
   }
   return (int)hipErrorInvalidValue;
@@ -1603,17 +1611,17 @@ static int launch_gemv_ci(int ci, const GemvArgs& a, hipStream_t s) {
 // when a wave would otherwise hold more than three items in registers.
 // Returns false when no plan keeps every wave at <= 3 items.
 struct MgPlan { int W, nb, nif, ept; };
-static bool mg_plan(const GemvArgs& a, int pro, MgPlan& p) {
-  const int K = a.Kp * 64, G = a.N / 8;
+static bool mg_plan(const GemvArgs& a, int pro, int ci, MgPlan& p) {
+  const int K = a.Kp * 64, GR = 64 / ci, G = a.N / GR;
   p.W = K > 2048 ? 16 : 4;
-  if (pro != PRO_NONE && p.W != 4) return false;
+  if ((pro != PRO_NONE || ci != 8) && p.W != 4) return false;
   const int ept = (K + 64 * p.W - 1) / (64 * p.W);
   p.ept = ept <= 2 ? ept : ept <= 4 ? 4 : ept <= 5 ? 5 : 8;
   int nb = min(G, p.W == 4 ? 512 : 256);
   for (;;) {
     const int gpb = (G + nb - 1) / nb;
     const int nif = (gpb * a.KpS + p.W - 1) / p.W;
-    if (nif <= 3 && gpb * 8 <= kMgRows) {
+    if (nif <= 3 && gpb * GR <= kMgRows) {
       p.nb = nb;
       p.nif = nif;
       return true;
@@ -1623,50 +1631,56 @@ static bool mg_plan(const GemvArgs& a, int pro, MgPlan& p) {
   }
 }
 
-template <int PRO, int EPI, int W, int NIF>
+template <int PRO, int EPI, int CI, int W, int NIF>
 static int launch_mg_ept(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
   const size_t lds = (size_t)a.Kp * kXPad * sizeof(float);
   switch (p.ept) {
 #define GG_MG_EPT(E) \
-    case E: hipLaunchKernelGGL((k_gemv_mg<PRO, EPI, W, NIF, E>), dim3(p.nb), dim3(64 * W), lds, s, a); break;
+    case E: hipLaunchKernelGGL((k_gemv_mg<PRO, EPI, CI, W, NIF, E>), dim3(p.nb), dim3(64 * W), lds, s, a); break;
     GG_MG_EPT(1) GG_MG_EPT(2) GG_MG_EPT(4) GG_MG_EPT(5) GG_MG_EPT(8)
 #undef GG_MG_EPT
     default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();
 }
-template <int PRO, int EPI, int W>
+template <int PRO, int EPI, int CI, int W>
 static int launch_mg_nif(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
   switch (p.nif) {
-    case 1: return launch_mg_ept<PRO, EPI, W, 1>(a, p, s);
-    case 2: return launch_mg_ept<PRO, EPI, W, 2>(a, p, s);
-    case 3: return launch_mg_ept<PRO, EPI, W, 3>(a, p, s);
+    case 1: return launch_mg_ept<PRO, EPI, CI, W, 1>(a, p, s);
+    case 2: return launch_mg_ept<PRO, EPI, CI, W, 2>(a, p, s);
+    case 3: return launch_mg_ept<PRO, EPI, CI, W, 3>(a, p, s);
   }
   return (int)hipErrorInvalidValue;
 }
-static int launch_mg(int pro, int epi, const GemvArgs& a, const MgPlan& p, hipStream_t s) {
-  if (pro == PRO_ATTN_MERGE) return launch_mg_nif<PRO_ATTN_MERGE, EPI_OUT, 4>(a, p, s);
+template <int CI>
+static int launch_mg_ci(int pro, int epi, const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  if (pro == PRO_ATTN_MERGE) return launch_mg_nif<PRO_ATTN_MERGE, EPI_OUT, CI, 4>(a, p, s);
   if (pro == PRO_NONE) {
-    return p.W == 4 ? launch_mg_nif<PRO_NONE, EPI_OUT, 4>(a, p, s) : launch_mg_nif<PRO_NONE, EPI_OUT, 16>(a, p, s);
+    if (CI == 8 && p.W == 16) return launch_mg_nif<PRO_NONE, EPI_OUT, 8, 16>(a, p, s);
+    return launch_mg_nif<PRO_NONE, EPI_OUT, CI, 4>(a, p, s);
   }
-  if (epi == EPI_GEGLU) return launch_mg_nif<PRO_RESID_NORM, EPI_GEGLU, 4>(a, p, s);
-  if (pro == PRO_EMBED_NORM) return launch_mg_nif<PRO_EMBED_NORM, EPI_OUT, 4>(a, p, s);
-  return launch_mg_nif<PRO_RESID_NORM, EPI_OUT, 4>(a, p, s);
+  if (epi == EPI_GEGLU) return launch_mg_nif<PRO_RESID_NORM, EPI_GEGLU, CI, 4>(a, p, s);
+  if (pro == PRO_EMBED_NORM) return launch_mg_nif<PRO_EMBED_NORM, EPI_OUT, CI, 4>(a, p, s);
+  return launch_mg_nif<PRO_RESID_NORM, EPI_OUT, CI, 4>(a, p, s);
+}
+static int launch_mg(int pro, int epi, int ci, const GemvArgs& a, const MgPlan& p, hipStream_t s) {
+  return ci == 2 ? launch_mg_ci<2>(pro, epi, a, p, s) : launch_mg_ci<8>(pro, epi, a, p, s);
 }
 
 int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  if (a.Kp * 64 > kMaxK || a.Kp <= 0 || a.N <= 0 || (ci != 1 && ci != 8) || a.N % (64 / ci) ||
+  if (a.Kp * 64 > kMaxK || a.Kp <= 0 || a.N <= 0 || (ci != 1 && ci != 2 && ci != 8) || a.N % (64 / ci) ||
       a.KpS != (a.Kp + ci - 1) / ci)
     return (int)hipErrorInvalidValue;
   if (pro != PRO_NONE && a.Kp * 64 > kMaxEPT / 4 * 256) return (int)hipErrorInvalidValue;
   if (epi == EPI_GEGLU && pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
   MgPlan plan;
   if (pro == PRO_ATTN_MERGE) {   // only the multi-group kernel merges: K = n_q * 256 <= 1024 on 256 threads
-    if (ci != 8 || a.Kp * 64 > kAttnMaxQ * kHeadDim || a.Kp % 4 || !mg_plan(a, pro, plan)) return (int)hipErrorInvalidValue;
-    return launch_mg(pro, epi, a, plan, s);
+    if (ci == 1 || a.Kp * 64 > kAttnMaxQ * kHeadDim || a.Kp % 4 || !mg_plan(a, pro, ci, plan))
+      return (int)hipErrorInvalidValue;
+    return launch_mg(pro, epi, ci, a, plan, s);
   }
-  if (ci == 8 && mg_plan(a, pro, plan)) return launch_mg(pro, epi, a, plan, s);
+  if (ci != 1 && mg_plan(a, pro, ci, plan)) return launch_mg(pro, epi, ci, a, plan, s);
   if (epi == EPI_GEGLU) return launch_gemv_ci<PRO_RESID_NORM, EPI_GEGLU>(ci, a, s);
   if (pro == PRO_NONE) return launch_gemv_ci<PRO_NONE, EPI_OUT>(ci, a, s);
   if (pro == PRO_EMBED_NORM) return launch_gemv_ci<PRO_EMBED_NORM, EPI_OUT>(ci, a, s);
@@ -1719,7 +1733,9 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
 }
 
 int launch_gemm(int epi, const GemmArgs& a, void* stream) {
-  if (a.M < 1 || a.N % kGBN || a.K != a.Kp * 64 || a.KpS != (a.Kp + 7) / 8) return (int)hipErrorInvalidValue;
+  if (a.M < 1 || a.N % kGBN || a.K != a.Kp * 64 || (a.GR != 8 && a.GR != 32) ||
+      a.KpS != (a.Kp + 64 / a.GR - 1) / (64 / a.GR))
+    return (int)hipErrorInvalidValue;
   dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM);
   if (epi == EPI_OUT) hipLaunchKernelGGL(k_gemm<EPI_OUT>, grid, dim3(256), 0, (hipStream_t)stream, a);
   else hipLaunchKernelGGL(k_gemm<EPI_GEGLU>, grid, dim3(256), 0, (hipStream_t)stream, a);

@@ -33,9 +33,9 @@ enum Q8Idx { Q_ATTN_Q, Q_ATTN_K, Q_ATTN_V, Q_ATTN_O, Q_GATE, Q_UP, Q_DOWN, Q_NQ8
 const char* kQ8Names[Q_NQ8] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
 
 struct Layer {
-  uint8_t* qkv = nullptr;   // fused [q | k | v] rows, pair-interleaved
+  uint8_t* qkv = nullptr;   // fused [q | k | v] rows, item-planar
   uint8_t* o = nullptr;
-  uint8_t* gu = nullptr;    // gate/up rows interleaved 32 + 32 per group (CI = 1)
+  uint8_t* gu = nullptr;    // gate/up rows interleaved GR/2 + GR/2 per row group
   uint8_t* down = nullptr;
   float* norm[N_NNORM] = {};
   float* kc = nullptr;
@@ -114,7 +114,7 @@ struct gg_ctx {
   hipGraphExec_t g_fwd = nullptr, g_sel = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int probe_kind = GG_PROBE_NONE, probe_layer = 0;
-  hipEvent_t probe_ev[2] = {nullptr, nullptr};
+  hipEvent_t probe_ev[4] = {nullptr, nullptr, nullptr, nullptr};   // kernel bracket [0, 1], empty bracket [2, 3]
   bool probe_done = false;
   bool finalized = false, lost = false, timed = false;
   bool use_graphs = true;   // GG_NO_GRAPH=1: launch the same kernels directly (profilers)
@@ -184,7 +184,11 @@ struct ProbeScope {
   gg_ctx* c;
   bool on;
   ProbeScope(gg_ctx* c_, int kind, int layer) : c(c_), on(c_->probe_kind == kind && (layer < 0 || c_->probe_layer == layer)) {
-    if (on) (void)hipEventRecordWithFlags(c->probe_ev[0], c->stream, hipEventRecordExternal);
+    if (on) {
+      (void)hipEventRecordWithFlags(c->probe_ev[2], c->stream, hipEventRecordExternal);
+      (void)hipEventRecordWithFlags(c->probe_ev[3], c->stream, hipEventRecordExternal);
+      (void)hipEventRecordWithFlags(c->probe_ev[0], c->stream, hipEventRecordExternal);
+    }
   }
   ~ProbeScope() {
     if (on) (void)hipEventRecordWithFlags(c->probe_ev[1], c->stream, hipEventRecordExternal);
@@ -367,6 +371,7 @@ GemmArgs gemm_base(const float* A, const uint8_t* W, const Q8Layout& L, int M, f
   g.K = L.K;
   g.Kp = L.Kp;
   g.KpS = L.KpS;
+  g.GR = L.GR;
   g.C = C;
   return g;
 }
@@ -517,7 +522,7 @@ gg_ctx* gg_create(const gg_config* cfg) {
   c->lay_embd = q8_layout(c->V, c->H, 1);
   c->lay_qkv = q8_layout(c->NQKV, c->H, 8);
   c->lay_o = q8_layout(c->H, c->QD, 8);
-  c->lay_gu = q8_layout(2 * c->I, c->H, 8);
+  c->lay_gu = q8_layout(2 * c->I, c->H, padfree_ci(c->H / 64));
   c->lay_down = q8_layout(c->H, c->I, 8);
   if (dalloc(c, &c->embd, c->lay_embd.bytes()) || dalloc(c, &c->out_norm, (size_t)c->H * 4)) return fail(0);
   for (Layer& Ly : c->layers) {
@@ -726,7 +731,9 @@ int gg_finalize(gg_ctx* c) {
   memset(c->h_st, 0, sizeof(DevState));
   for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreate(&c->ev[i]));
   if (c->probe_kind != GG_PROBE_NONE)
-    for (int i = 0; i < 2; ++i) GG_HIP(c, hipEventCreate(&c->probe_ev[i]));
+    // timing-only events: no system-scope fence (cache write-back/invalidate)
+    // around the bracketed launch
+    for (int i = 0; i < 4; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->probe_ev[i], hipEventDisableSystemFence));
 
   const char* ng = getenv("GG_NO_GRAPH");
   c->use_graphs = !(ng && ng[0] == '1');
@@ -890,6 +897,13 @@ int gg_probe_elapsed(gg_ctx* c, float* ms) {
   if (c->probe_kind == GG_PROBE_NONE || !ms) return set_err(c, GG_ERR_INVALID, "no probe set");
   if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
   GG_HIP(c, hipEventElapsedTime(ms, c->probe_ev[0], c->probe_ev[1]));
+  return GG_OK;
+}
+int gg_probe_overhead(gg_ctx* c, float* ms) {
+  GG_TRY(check_ready(c));
+  if (c->probe_kind == GG_PROBE_NONE || !ms) return set_err(c, GG_ERR_INVALID, "no probe set");
+  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  GG_HIP(c, hipEventElapsedTime(ms, c->probe_ev[2], c->probe_ev[3]));
   return GG_OK;
 }
 

@@ -95,6 +95,7 @@ _SIGS = {
     "gg_last_timing": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
     "gg_set_probe": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32]),
     "gg_probe_elapsed": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
+    "gg_probe_overhead": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
     "gg_last_error": (ctypes.c_char_p, [_P]),
     "gg_destroy": (None, [_P]),
     "gg_q8_0_packed_size": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
@@ -220,6 +221,12 @@ class Engine:
     def probe_elapsed_ms(self) -> float:
         v = ctypes.c_float()
         _check(self.ctx, lib().gg_probe_elapsed(self.ctx, ctypes.byref(v)))
+        return v.value
+
+    def probe_overhead_ms(self) -> float:
+        """Device time of an empty event bracket recorded right before the probe."""
+        v = ctypes.c_float()
+        _check(self.ctx, lib().gg_probe_overhead(self.ctx, ctypes.byref(v)))
         return v.value
 
     def close(self):
