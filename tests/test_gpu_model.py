@@ -184,3 +184,90 @@ def test_1b_full_size_step_with_shared_kv(gpu, mode, ctx, span):
     assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL
     assert nxt == ref
     e.close()
+
+
+@pytest.mark.parametrize("mode", ["reference", "gemma3"])
+def test_tiny_gpu_matches_golden(gpu, tiny_model, mode):
+    """The GPU path against the committed float64 golden vectors
+    (tests/golden/tiny_<mode>.npz): per-layer hidden, normed and logits after
+    the prompt within 1e-4, and the same 12 greedy ids."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"tiny_{mode}.npz"),
+                allow_pickle=False)
+    shape = synth.TINY.reference_mode() if mode == "reference" else synth.TINY.gemma3_mode(window=7)
+    e = engine(shape, tiny_model)
+    e.prefill(g["prompt"], 0)
+    for l in range(shape.layers):
+        assert rel(e.read(capi.READ_LAYER_HIDDEN, l), g["hist"][l]) < 1e-4, l
+    assert rel(e.read(capi.READ_NORMED), g["normed"]) < 1e-4
+    tok = e.select()
+    assert rel(e.read(capi.READ_LOGITS), g["logits"]) < 1e-4
+    toks, pos = [], len(g["prompt"])
+    for _ in range(len(g["greedy"])):
+        toks.append(tok)
+        tok = e.step(tok, pos)
+        pos += 1
+    assert toks == g["greedy"].tolist()
+    e.close()
+
+
+def test_1b_32k_three_turns_sampling(gpu):
+    """Gemma-3-1B at contextLength 32768, gemma3 attention: three chained turns
+    whose prompts fill ~32K positions of KV, sampling with T=0.7, topP=0.9,
+    rep=1.2 and a seeded u stream (generate(), engine.ts:957-1031: per-turn
+    penalty set = the turn's prompt + its generated ids; the last generated id
+    of a turn is not written to the KV cache).
+    * every sampled id equals the reference's selection (topk256 + host
+      sampler, engine.ts:854-901, in the oracle) on the GPU's own logits;
+    * KV reuse: a second engine that prefills every id the first one wrote
+      (one call) and then takes the same last step reproduces its logits and
+      id bit for bit."""
+    shape = synth.GEMMA3_1B.with_ctx(32768).gemma3_mode()
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    e = engine(shape, t)
+    rng = np.random.default_rng(55)
+    opts = (0.7, 0.9, 1.2)
+    prompts = [synth.prompt_ids(n, seed=300 + i, vocab=shape.vocab) for i, n in enumerate([16384, 8192, 8100])]
+    kv_ids, kv_pos = [], 0
+    last = None
+    for turn, p in enumerate(prompts):
+        say("32k turn", turn, "prefill", len(p), "at", kv_pos)
+        e.penalty_reset()
+        e.penalty_add(p)
+        e.prefill(p, kv_pos)
+        kv_ids += [int(x) for x in p]
+        kv_pos += len(p)
+        seen = [int(x) for x in p]
+        u = float(rng.random())
+        tok = e.select(*opts, u)
+        vals, ids = orc.topk256(e.read(capi.READ_LOGITS))
+        assert tok == orc.sample_candidates(vals, ids, seen, *opts, u), f"turn {turn} first id"
+        seen.append(tok)
+        writes = 0
+        for k in range(7):
+            pos = kv_pos + writes
+            u = float(rng.random())
+            nxt = e.step(tok, pos, *opts, u)
+            kv_ids.append(tok)
+            writes += 1
+            logits = e.read(capi.READ_LOGITS)
+            vals, ids = orc.topk256(logits)
+            assert nxt == orc.sample_candidates(vals, ids, seen, *opts, u), f"turn {turn} step {k}"
+            seen.append(nxt)
+            last = (tok, pos, u, seen[:-1], logits, nxt)
+            tok = nxt
+        kv_pos += writes
+    assert kv_pos == len(kv_ids) and kv_pos < shape.ctx - 10
+    e.close()
+    # KV reuse: one prefill of everything but the last written id, then that step
+    say("32k replay", len(kv_ids) - 1)
+    b = engine(shape, t)
+    b.penalty_reset()
+    b.penalty_add(last[3])
+    b.prefill(kv_ids[:-1], 0)
+    tok, pos, u, _, logits, nxt = last
+    assert b.step(tok, pos, *opts, u) == nxt
+    assert np.array_equal(b.read(capi.READ_LOGITS), logits)
+    b.close()
