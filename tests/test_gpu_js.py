@@ -1,0 +1,74 @@
+"""The JavaScript host on the GPU through the Node-API binding: two generate()
+turns (greedy, then sampled with a seeded draw) on a tiny GGUF written by
+gemma_amd.gguf. The binding calls the host made are replayed through the
+Python C-ABI binding and must give the same ids; the greedy turn must also
+match the oracle."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from gemma_amd import capi, synth
+from oracle import oracle as orc
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+NODE = shutil.which("node")
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+@pytest.mark.parametrize("attention", ["reference", "gemma3"])
+def test_js_host_on_gpu(gpu, tmp_path, attention):
+    say("js host", attention)
+    shape = synth.TINY.with_ctx(256)
+    tensors = synth.make_model(shape, seed=9)
+    g = str(tmp_path / "tiny.gguf")
+    synth.write_model_gguf(g, shape, tensors=tensors)
+    r = subprocess.run([NODE, os.path.join(HERE, "js", "gpu_generate.js"), g, attention], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    log = out["log"]
+    run_shape = shape.gemma3_mode(window=512) if attention == "gemma3" else shape.reference_mode()
+
+    # replay the same calls through the Python binding of the C-ABI
+    e = capi.Engine(run_shape.gg_config())
+    e.upload_model(tensors)
+    e.finalize()
+    for c in log:
+        if c["op"] == "prefill":
+            e.prefill(np.array(c["ids"], np.int32), c["pos"])
+        elif c["op"] == "penaltyReset":
+            e.penalty_reset()
+        elif c["op"] == "penaltyAdd":
+            e.penalty_add(c["ids"])
+        elif c["op"] == "select":
+            assert e.select(c["t"], c["p"], c["r"], c["u"]) == c["id"]
+        else:
+            assert e.step(c["tok"], c["pos"], c["t"], c["p"], c["r"], c["u"]) == c["id"]
+    e.close()
+
+    # the greedy first turn against the oracle
+    o = orc.OracleModel(run_shape, tensors)
+    first = log[[c["op"] for c in log].index("prefill")]
+    o.prefill(np.array(first["ids"], np.int32), 0)
+    sel = [c for c in log if c["op"] in ("select", "step") and c["t"] == 0]
+    seen = list(first["ids"])           # the turn's penalty set: its prompt + the selected ids
+    assert sel[0]["op"] == "select"
+    assert o.select(0.0, sel[0]["p"], sel[0]["r"], 0.0, seen=seen) == sel[0]["id"]
+    seen.append(sel[0]["id"])
+    for c in sel[1:]:
+        o.forward(c["tok"], c["pos"])
+        assert o.select(0.0, c["p"], c["r"], 0.0, seen=seen) == c["id"]
+        seen.append(c["id"])
+    o.close()
+    # positions: the second turn's prefill starts where the first turn's KV ends
+    pf = [c for c in log if c["op"] == "prefill"]
+    greedy_writes = sum(1 for c in sel if c["op"] == "step")
+    assert pf[1]["pos"] == len(pf[0]["ids"]) + greedy_writes
+    assert pf[1]["ids"][0] != 2        # the turn suffix has no BOS

@@ -1,4 +1,4 @@
-"""Build recipe for libgg.so (gfx950) and the N-API addon.
+"""Build recipe for libgg.so (gfx950) and the Node-API binding of the JavaScript host.
 
 Called by __graft_entry__.build(); compiles every time it is called.
 """
@@ -42,5 +42,23 @@ def build_lib() -> str:
     return out
 
 
+NODE_INCLUDE = "/usr/include/node"
+
+
+def build_napi() -> str:
+    """gg_napi.node: the Node-API binding (C, gcc) linked against libgg.so in
+    the same directory. Returns the path, or "" when the Node headers are absent."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return ""
+    out = os.path.join(LIBDIR, "gg_napi.node")
+    tmp = out + ".tmp"
+    _run(["gcc", "-shared", "-fPIC", "-O2", "-std=c11", "-Wall", "-Werror", "-I", NODE_INCLUDE,
+          "-I", os.path.join(ROOT, "include"), os.path.join(PKG, "js", "gg_napi.c"), "-o", tmp,
+          "-L", LIBDIR, "-lgg", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build_lib())
+    print(build_napi())

@@ -1,0 +1,211 @@
+'use strict';
+// The JavaScript host: the reference's public engine API (index.ts:34-38,
+// types.ts:86-97, engine.ts:31-1078) over the libgg.so C-ABI through the
+// Node-API binding (gg_napi.node). The WebGPU device, pipelines, buffers and
+// bind groups of engine.ts are replaced by one context of the binding; what
+// stays here is what stays in JavaScript in the reference: GGUF parsing, the
+// tokenizer, the chat template, conversation / KV-position bookkeeping, stop
+// ids, the Math.random() draw and the per-turn penalty set.
+const fs = require('fs');
+const path = require('path');
+
+const gguf = require('./gguf');
+const { Tokenizer } = require('./tokenizer');
+const { buildChatPrompt, turnSuffix } = require('./conversation');
+
+const GG_ATTN_REFERENCE = 0;
+const GG_ATTN_GEMMA3 = 1;
+
+// Defaults of types.ts:19-36 (Gemma-3 270M), updated from the GGUF.
+function defaultConfig() {
+  return {
+    hidden_size: 640, q_dim: 1024, kv_dim: 256, num_q_heads: 4, num_kv_heads: 1, head_dim: 256,
+    intermediate_size: 2048, vocab_size: 262144, num_layers: 18, context_length: 2048,
+    rms_norm_eps: 1e-6, rope_theta_global: 1000000.0, rope_theta_swa: 1000000.0, swa_period: 6,
+    sliding_window: 0,
+  };
+}
+
+function loadBinding(dir) {
+  const p = path.join(dir || path.join(__dirname, '..', 'lib'), 'gg_napi.node');
+  return require(p);   // throws when the HIP library or the binding is missing
+}
+
+class GemmaEngineImpl {
+  constructor(options) {
+    this.config = defaultConfig();
+    if (options.contextLength) this.config.context_length = options.contextLength;
+    this.onProgress = options.onProgress;
+    this.gg = options.backend || loadBinding(options.bindingDir);
+    this.random = options.random || Math.random;
+    // 'reference' (one theta, full attention: src/ as shipped) or 'gemma3'
+    // (local layers: theta 1e4, 512-position window)
+    this.attention = options.attention || 'reference';
+    this.prefillBatch = options.prefillBatch || 0;
+    this.ctx = null;
+    this.conversationHistory = [];
+    this.kvPosition = 0;
+    this.deviceLost = false;
+  }
+
+  reportProgress(loaded, total, status) {
+    if (this.onProgress) this.onProgress({ loaded: loaded, total: total, status: status });
+  }
+
+  // init(): the model is a path to a local .gguf file (no network here);
+  // tensors stream from the file to the device one at a time.
+  async init(options) {
+    const file = options.model;
+    if (!file || !fs.existsSync(file)) throw new Error('model must be the path of a .gguf file: ' + file);
+    const fd = fs.openSync(file, 'r');
+    try {
+      this.reportProgress(0, 1, 'Reading header...');
+      const g = gguf.parseHeader(fd);
+      const cfg = gguf.configFromGGUF(g, this.config, options.contextLength);
+      const emb = g.tensors.find((t) => t.name === 'token_embd.weight');
+      if (!emb) throw new Error('GGUF has no token_embd.weight');
+      cfg.vocab_size = emb.dims[1];
+      if (this.attention === 'gemma3') {
+        cfg.rope_theta_swa = 10000.0;
+        cfg.sliding_window = cfg.file_sliding_window || 512;
+      }
+      this.config = cfg;
+      this.tokenizer = Tokenizer.fromGGUF(g);
+      this.ctx = this.call(() => this.gg.create({
+        hidden_size: cfg.hidden_size, num_layers: cfg.num_layers, num_q_heads: cfg.num_q_heads,
+        num_kv_heads: cfg.num_kv_heads, head_dim: cfg.head_dim, intermediate_size: cfg.intermediate_size,
+        vocab_size: cfg.vocab_size, context_length: cfg.context_length, rms_norm_eps: cfg.rms_norm_eps,
+        rope_theta_global: cfg.rope_theta_global, rope_theta_local: cfg.rope_theta_swa,
+        swa_period: cfg.swa_period, sliding_window: cfg.sliding_window,
+        attention_mode: this.attention === 'gemma3' ? GG_ATTN_GEMMA3 : GG_ATTN_REFERENCE,
+        prefill_batch: this.prefillBatch,
+      }));
+      const total = g.tensors.reduce((a, t) => a + gguf.tensorByteSize(t), 0);
+      let loaded = 0;
+      for (const t of g.tensors) {
+        const bytes = gguf.readTensor(fd, g, t);
+        this.call(() => this.gg.upload(this.ctx, t.name, t.type, t.dims, bytes));
+        loaded += bytes.length;
+        this.reportProgress(loaded, total, 'Uploading weights...');
+      }
+      this.call(() => this.gg.finalize(this.ctx));
+      this.reportProgress(total, total, 'Ready');
+    } finally {
+      fs.closeSync(fd);
+    }
+  }
+
+  // Failures of the binding: GG_ERR_DEVICE_LOST sets deviceLost (engine.ts:134-137).
+  call(fn) {
+    try {
+      return fn();
+    } catch (e) {
+      this.noteError(e);
+      throw e;
+    }
+  }
+
+  async callAsync(fn) {
+    try {
+      return await fn();
+    } catch (e) {
+      this.noteError(e);
+      throw e;
+    }
+  }
+
+  noteError(e) {
+    if (e && e.code === 'GG_ERR_DEVICE_LOST') this.deviceLost = true;
+  }
+
+  addUserMessage(text) {
+    this.conversationHistory.push({ role: 'user', text: text });
+  }
+
+  // generate(): engine.ts:957-1031 -- prompt (first turn) or turn suffix,
+  // overflow reset at contextLength - 10, prefill, first token from the LM
+  // head, then one forward + select per token until a stop id, the abort
+  // signal, maxTokens or the end of the context.
+  async *generate(options) {
+    const o = options || {};
+    if (this.deviceLost) throw new Error('GPU device lost - call dispose() and recreate the engine');
+    const temperature = o.temperature === undefined ? 0.7 : o.temperature;
+    const topP = o.topP === undefined ? 0.9 : o.topP;
+    const repPenalty = o.repPenalty === undefined ? 1.2 : o.repPenalty;
+    const maxTokens = o.maxTokens === undefined ? 32768 : o.maxTokens;
+    const toolsJson = o.toolsJson === undefined ? '[]' : o.toolsJson;
+    const signal = o.signal;
+    // the uniform draw is taken only when sampling (engine.ts:878,894)
+    const draw = () => (temperature === 0 ? 0 : this.random());
+
+    let newTokens;
+    if (this.kvPosition === 0) {
+      newTokens = this.tokenizer.encode(buildChatPrompt(this.conversationHistory, toolsJson));
+    } else {
+      const lastUser = this.conversationHistory[this.conversationHistory.length - 1];
+      newTokens = this.tokenizer.encode(turnSuffix(lastUser.text)).slice(1);   // no BOS
+    }
+    if (this.kvPosition + newTokens.length >= this.config.context_length - 10) {
+      const lastUser = this.conversationHistory[this.conversationHistory.length - 1];
+      this.conversationHistory = [{ role: 'user', text: lastUser.text }];
+      newTokens = this.tokenizer.encode(buildChatPrompt(this.conversationHistory, toolsJson));
+      this.call(() => this.gg.resetKV(this.ctx));
+      this.kvPosition = 0;
+    }
+
+    // the turn's repetition-penalty set starts as its prompt tokens; the
+    // device adds every selected id (allTokens, engine.ts:989,994,1021)
+    const ids = Int32Array.from(newTokens);
+    this.call(() => this.gg.penaltyReset(this.ctx));
+    this.call(() => this.gg.penaltyAdd(this.ctx, ids));
+    await this.callAsync(() => this.gg.prefill(this.ctx, ids, this.kvPosition));
+    this.kvPosition += newTokens.length;
+
+    let next = await this.callAsync(() => this.gg.select(this.ctx, temperature, topP, repPenalty, draw()));
+    const endCall = this.tokenizer.funcTokens['<end_function_call>'];
+    const generated = [next];
+    let writes = 0;
+    yield this.tokenizer.decodeToken(next);
+
+    for (let step = 1; step < maxTokens; step++) {
+      if (next === 1 || next === 0 || next === 106) break;
+      if (endCall !== undefined && next === endCall) break;
+      if (signal && signal.aborted) break;
+      const pos = this.kvPosition + writes;
+      if (pos >= this.config.context_length - 1) break;
+      const tok = next;
+      next = await this.callAsync(() => this.gg.step(this.ctx, tok, pos, temperature, topP, repPenalty, draw()));
+      writes++;
+      if (next === 1 || next === 0 || next === 106) break;
+      if (endCall !== undefined && next === endCall) {
+        generated.push(next);
+        break;
+      }
+      generated.push(next);
+      yield this.tokenizer.decodeToken(next);
+    }
+    this.conversationHistory.push({ role: 'model', text: this.tokenizer.decodeTokens(generated) });
+    this.kvPosition += writes;
+  }
+
+  resetConversation() {
+    this.conversationHistory = [];
+    this.kvPosition = 0;
+    if (this.ctx) this.call(() => this.gg.resetKV(this.ctx));
+  }
+
+  dispose() {
+    if (this.ctx) this.gg.destroy(this.ctx);
+    this.ctx = null;
+  }
+}
+
+async function createGemmaEngine(options) {
+  const o = options || {};
+  const engine = new GemmaEngineImpl(o);
+  await engine.init(o);
+  return engine;
+}
+
+module.exports = { createGemmaEngine: createGemmaEngine, GemmaEngineImpl: GemmaEngineImpl,
+  defaultConfig: defaultConfig };
