@@ -31,9 +31,9 @@ constexpr int kPairBytes = 68;
 constexpr int kColBytes = 64 * kPairBytes;   // one wavefront step: 4352 bytes
 constexpr int kMaxK = 8192;          // largest GEMV input (x staged in LDS)
 constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
-constexpr int kAttnChunk = 32;       // base positions per attention block (4 waves x 8)
-constexpr int kAttnMaxChunks = 256;  // attention split-K chunks per query (batched prefill bound)
+constexpr int kAttnChunk = 32;       // base positions per decode attention block (4 waves x 8)
 constexpr int kDecMaxChunks = 64;    // decode attention chunks per token (16 while the span is <= 4096)
+constexpr int kMaxContext = 65536;   // largest context_length
 
 // Byte offset of dword j (0..16) of slot s (0..63) inside a 4352-byte item.
 inline constexpr int plane_offset(int j, int s) {
@@ -121,14 +121,15 @@ struct AttnArgs {
   float scale;             // 1/sqrt(head_dim)
   const DevState* st;
   float* part;             // decode: o [kDecMaxChunks][kAttnMaxQ][256] then (m, l) [kDecMaxChunks][kAttnMaxQ][2];
-                           // batched prefill: [row][kPrefillChunks][n_q][2 + 256]
-  unsigned int* counter;   // batched prefill: arrivals of a row's chunk blocks (reset by the last)
-  float* attn_out;         // [n_q * 256]
-  float* q_dbg;            // optional: normed+roped q of this token
-  // batched prefill (k_attn<true>): query row r = blockIdx.y sits at position
-  // pf_start + r; K/V of every prompt position are already in the cache
+                           // batched prefill: (m, l, o[256]) [row][kPrefillChunks][n_q]
+  float* attn_out;         // decode [n_q * 256]; batched prefill [row][n_q * 256]
+  float* q_dbg;            // decode, optional: normed+roped q of this token
+  // batched prefill: prompt row r sits at position pf_start + r; q of every
+  // row is already normed + roped in `qkv`, K/V of every position are in the
+  // cache; keys of a 16-row query tile are split in chunks of pf_chunk
   int pf_start;
-  int max_chunks;          // batched prefill: chunks per query (kPrefillChunks)
+  int pf_rows;
+  int pf_chunk;
 };
 
 // Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W item-planar (GR = 8 or 32).
@@ -155,9 +156,10 @@ struct RowArgs {
   float* res_out;          // [M][H] new residual stream
   float* x_out;            // [M][H] normed GEMM input
   float* last_hidden;      // optional: row M-1 of res_out (per-layer history)
-  // KV: k/v of each row into the cache
+  // KV: k/v of each row into the cache, q heads normed + roped in place
   const float* qkv;
   int n_q;
+  const float* q_norm;
   const float* k_norm;
   const float* rope;
   float* k_cache;
@@ -207,6 +209,18 @@ int launch_gemm(int epi, const GemmArgs& a, void* stream);
 int launch_rows_embed(const RowArgs& a, void* stream);
 int launch_rows_resid(const RowArgs& a, void* stream);
 int launch_rows_kv(const RowArgs& a, void* stream);
-constexpr int kPrefillChunks = 16;   // chunks per query in the batched prefill
+constexpr int kPrefillChunks = 16;   // key chunks per query tile in the batched prefill attention
+constexpr int kPrefillMinChunk = 256;
+// Longest key span of a 16-row query tile of a prefill of M rows at `start`.
+inline int prefill_max_span(int window, int start, int M) {
+  const int full = start + M;
+  return window > 0 && window + 15 < full ? window + 15 : full;
+}
+// Keys per chunk: a multiple of 32, >= kPrefillMinChunk, at most kPrefillChunks chunks.
+inline int prefill_chunk(int window, int start, int M) {
+  const int span = prefill_max_span(window, start, M);
+  const int c = 32 * ((span + 32 * kPrefillChunks - 1) / (32 * kPrefillChunks));
+  return c > kPrefillMinChunk ? c : kPrefillMinChunk;
+}
 
 }  // namespace gg

@@ -1,23 +1,27 @@
 // gg_kernels.hip -- gfx950 (CDNA4) kernels of the Gemma-3 Q8_0 token loop.
 //
 // One forward pass over a token is five kernels per layer:
-//   k_gemv<EMBED_NORM|RESID_NORM, OUT>  fused QKV projection; its prologue
+//   k_gemv_mg<EMBED_NORM|RESID_NORM, OUT>  fused QKV projection; its prologue
 //        finishes the previous layer (post-FFN norm + residual) and applies
 //        attn_norm (engine.ts:768-774, 794)
-//   k_attn          QK-norm + RoPE + KV store + one chunk of decode attention
-//                   per block; the last block merges the chunks (engine.ts:775-783)
-//   k_gemv<NONE, OUT>          attention output projection (engine.ts:784)
-//   k_gemv<RESID_NORM, GEGLU>  post-attn norm + residual + ffn_norm, gate and
-//                   up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
-//   k_gemv<NONE, OUT>          down projection (engine.ts:793)
+//   k_attn_dec      QK-norm + RoPE + KV store + one chunk of decode attention
+//                   per block, chunk partials to memory (engine.ts:775-783)
+//   k_gemv_mg<ATTN_MERGE, OUT>  merges the attention chunks in its prologue,
+//                   then the attention output projection (engine.ts:784)
+//   k_gemv_mg<RESID_NORM, GEGLU>  post-attn norm + residual + ffn_norm, gate
+//                   and up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
+//   k_gemv_mg<NONE, OUT>       down projection (engine.ts:793)
 // then k_final (post-FFN norm + residual + output_norm, engine.ts:794-801),
 // and for a sampled step the LM head GEMV plus k_select1/k_select2
 // (engine.ts:817-901).
 //
+// A batched prefill runs per layer the fp32-MFMA GEMMs (k_gemm), the row
+// kernels (norms, residuals, QK-norm + RoPE + KV store) and the MFMA
+// attention k_attn_pf (+ k_attn_pf_merge for long spans).
+//
 // On this multi-XCD part a device-scope fence is a whole-L2 write-back, so
-// kernels never fence. The one in-kernel cross-block step (the attention
-// chunk merge) exchanges data with write-through device-scope stores/loads
-// and a device-scope counter; everything else is a graph kernel boundary.
+// kernels never fence and never exchange data across blocks of one launch:
+// every cross-block step is a kernel boundary.
 //
 // All arithmetic is fp32 except the int8 weight payload (dequantised exactly
 // in registers) and the sampler's f64 steps, which mirror the JS host's.
@@ -574,371 +578,6 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention (one KV head, head_dim 256), one chunk of positions per
-// block. Block b covers [t0, t1) of the attended span [t_lo, pos]; the chunk
-// grows with the span so at most kAttnMaxChunks blocks are live. Every block
-// rebuilds q/k from the QKV output with the per-head RMSNorm + NEOX RoPE
-// (fusedPerHeadNormRope, shaders.ts:420-467); the block holding `pos` stores
-// k/v into the cache (kvCacheStore, shaders.ts:209-227) and reads them from
-// LDS. Scores/softmax/weighted-V follow shaders.ts:229-325 within the chunk
-// and leave (max, sum, o) per head; the last block to finish merges them.
-//
-// Scores: wave w takes P = 64/NQP positions at a time with one float4 of the
-// head per lane; the P*NQP = 64 partial dots per lane are finished by one
-// reduce-scatter butterfly (63 shuffles) after which lane l owns dot l.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void attn_span(const AttnArgs& a, int pos, int* t_lo, int* ch, int* nch) {
-  const int lo = a.window > 0 ? max(0, pos - a.window + 1) : 0;
-  const int span = pos - lo + 1;
-  const int c = kAttnChunk * ((span + kAttnChunk * a.max_chunks - 1) / (kAttnChunk * a.max_chunks));
-  *t_lo = lo;
-  *ch = c;
-  *nch = (span + c - 1) / c;
-}
-
-// Device-scope (write-through / L2-bypassing) accesses for the chunk
-// statistics that the last block of k_attn merges; unlike a device-scope
-// fence they do not write back the whole L2.
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Lane l of a wave works on position p = l / 8 of the wave's pass and on
-// dims [32 o, 32 o + 32) with o = l % 8 for the scores, and on dims
-// [4 l, 4 l + 4) of every position for the weighted sum of V.
-constexpr int kAttnP = 8;   // positions per wave pass
-constexpr int kQPad = 288;  // LDS floats per head: 8 octants of 32 dims + 4 pad each
-__device__ __forceinline__ int qidx(int d) { return (d >> 5) * 36 + (d & 31); }
-
-// PF = false: decode, one token at DevState.pos; the block holding pos also
-// norms/ropes k and stores k/v. PF = true: batched prefill, query row
-// blockIdx.y at pf_start + blockIdx.y, every K/V row already in the cache.
-template <bool PF>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
-  constexpr int NQ = kAttnMaxQ;
-  __shared__ float qs[NQ][kQPad];
-  __shared__ float ks[kQPad];
-  __shared__ float vs[kHeadDim];
-  __shared__ float pw[4][kAttnP * NQ];
-  __shared__ float wm[4][NQ], wl[4][NQ];
-  __shared__ float wo[4][NQ][kHeadDim];
-  __shared__ float sm[kAttnMaxChunks * NQ];
-  __shared__ float sf[kAttnMaxChunks * NQ];
-  __shared__ float hstat[NQ][2];
-  __shared__ int is_last;
-
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int nq = a.n_q;
-  const int nqd = nq * kHeadDim;
-  const int row = PF ? (int)blockIdx.y : 0;
-  const int pos = PF ? a.pf_start + row : a.st->pos;
-  const float* qkv = a.qkv + (size_t)row * (nqd + 2 * kHeadDim);
-  float* part = a.part + (size_t)row * a.max_chunks * kAttnMaxQ * (2 + kHeadDim);
-  unsigned int* counter = a.counter + row;
-  float* attn_out = a.attn_out + (size_t)row * nqd;
-  int t_lo, ch, nch;
-  attn_span(a, pos, &t_lo, &ch, &nch);
-  const int b = blockIdx.x;
-  if (b >= nch) return;
-  const int t0 = t_lo + b * ch;
-  const int t1 = min(t0 + ch, pos + 1);
-  const int kv_end = PF ? pos + 1 : pos;   // rows [.., kv_end) come from the cache
-  const int pl = lane >> 3, oc = lane & 7;
-
-  // 0. loads that do not depend on q: this wave's first pass of K rows (lane
-  // layout of the scores) and V rows (lane layout of the weighted sum), the
-  // QKV output, the norm weights and the RoPE frequencies
-  const int tb0 = t0 + wv * kAttnP;
-  float4 kr[8], vr[kAttnP];
-  {
-    const int t = tb0 + pl;
-    if (t < kv_end && t < t1) {
-      const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kr[j] = kp[j];
-    }
-#pragma unroll
-    for (int i = 0; i < kAttnP; ++i) {
-      const int tv = tb0 + i;
-      if (tv < kv_end && tv < t1) vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
-    }
-  }
-  const bool my_head = wv < nq;
-  const bool k_head = !PF && (wv == 0) && (b == nch - 1);
-  float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hx[i] = my_head ? qkv[wv * kHeadDim + lane + 64 * i] : 0.f;
-    nwt[i] = a.q_norm[lane + 64 * i];
-    kx[i] = PF ? 0.f : qkv[nqd + lane + 64 * i];
-    kwt[i] = a.k_norm[lane + 64 * i];
-  }
-  // RoPE table row of this position: cos(f32(pos) * freq[i]), sin(...)
-  const float* rt = a.rope + (size_t)pos * 2 * (kHeadDim / 2);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    cs[j] = rt[lane + 64 * j];
-    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
-  }
-  if (!PF && tid < kHeadDim) vs[tid] = qkv[nqd + kHeadDim + tid];
-
-  // 1. wave w: RMSNorm + NEOX RoPE of query head w (and, in the block that
-  // holds `pos`, wave 0 also of the key head) -- fusedPerHeadNormRope,
-  // shaders.ts:420-467. Lane owns dims lane + 64 i; pairs (i, i + 128).
-  auto norm_rope = [&](float* x, const float* w, float* dst) {
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
-    ss = wave_sum(ss);
-    const float rms = sqrtf(ss / (float)kHeadDim + a.eps);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) / rms;
-    // dims lane, lane+64 pair with lane+128, lane+192
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float x0 = x[j], x1 = x[j + 2];
-      dst[qidx(lane + 64 * j)] = x0 * cs[j] - x1 * sn[j];
-      dst[qidx(lane + 64 * j + 128)] = x0 * sn[j] + x1 * cs[j];
-    }
-  };
-  if (my_head) norm_rope(hx, nwt, qs[wv]);
-  else if (wv < NQ) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qs[wv][qidx(lane + 64 * i)] = 0.f;
-  }
-  if (k_head) norm_rope(kx, kwt, ks);
-  __syncthreads();
-
-  if (!PF && b == nch - 1) {
-    a.k_cache[(size_t)pos * kHeadDim + tid] = ks[qidx(tid)];
-    a.v_cache[(size_t)pos * kHeadDim + tid] = vs[tid];
-  }
-  if (!PF && b == 0 && a.q_dbg)
-    for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = qs[e >> 8][qidx(e & 255)];
-
-  // q slice of this lane's score layout: 4 heads x 32 dims in registers
-  float4 qr[NQ][8];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qr[h][j] = *(const float4*)&qs[h][36 * oc + 4 * j];
-
-  // 2. per-wave online softmax over passes of kAttnP positions
-  float m[NQ], l[NQ];
-  float4 o4[NQ];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
-    o4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  for (int tb = tb0; tb < t1; tb += 4 * kAttnP) {
-    const int t = tb + pl;
-    if (tb != tb0 && t < kv_end && t < t1) {
-      const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim + 32 * oc);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kr[j] = kp[j];
-    }
-    if (!PF && t == pos) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kr[j] = *(const float4*)&ks[36 * oc + 4 * j];
-    }
-#pragma unroll
-    for (int i = 0; i < kAttnP; ++i) {
-      const int tv = tb + i;
-      if (!PF && tv == pos) vr[i] = *(const float4*)&vs[4 * lane];
-      else if (tb != tb0 && tv < kv_end && tv < t1)
-        vr[i] = *(const float4*)(a.v_cache + (size_t)tv * kHeadDim + 4 * lane);
-    }
-    const bool valid = t < t1;
-    float sc[NQ];
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      float d = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        d = fmaf(qr[h][j].x, kr[j].x, d);
-        d = fmaf(qr[h][j].y, kr[j].y, d);
-        d = fmaf(qr[h][j].z, kr[j].z, d);
-        d = fmaf(qr[h][j].w, kr[j].w, d);
-      }
-      d += __shfl_xor(d, 1, 64);
-      d += __shfl_xor(d, 2, 64);
-      d += __shfl_xor(d, 4, 64);
-      sc[h] = (valid && h < nq) ? d * a.scale : -INFINITY;
-    }
-    float alpha[NQ], p[NQ];
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      float mx = sc[h];
-      mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m[h], mx);
-      alpha[h] = (m[h] == -INFINITY) ? 0.f : expf(m[h] - mn);
-      p[h] = (sc[h] == -INFINITY) ? 0.f : expf(sc[h] - mn);
-      float ps = p[h];
-      ps += __shfl_xor(ps, 8, 64);
-      ps += __shfl_xor(ps, 16, 64);
-      ps += __shfl_xor(ps, 32, 64);
-      l[h] = fmaf(l[h], alpha[h], ps);
-      m[h] = mn;
-    }
-    if (oc == 0) {
-#pragma unroll
-      for (int h = 0; h < NQ; ++h) pw[wv][pl * NQ + h] = p[h];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      o4[h].x *= alpha[h];
-      o4[h].y *= alpha[h];
-      o4[h].z *= alpha[h];
-      o4[h].w *= alpha[h];
-    }
-#pragma unroll
-    for (int i = 0; i < kAttnP; ++i) {
-      const float4 pp = *(const float4*)&pw[wv][i * NQ];
-      const float pv[4] = {pp.x, pp.y, pp.z, pp.w};
-      if (tb + i < t1) {
-#pragma unroll
-        for (int h = 0; h < NQ; ++h) {
-          o4[h].x = fmaf(pv[h], vr[i].x, o4[h].x);
-          o4[h].y = fmaf(pv[h], vr[i].y, o4[h].y);
-          o4[h].z = fmaf(pv[h], vr[i].z, o4[h].z);
-          o4[h].w = fmaf(pv[h], vr[i].w, o4[h].w);
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  // 3. merge the four waves (fixed order) into this chunk's (max, sum, o)
-  if (lane < NQ) {
-    float mm = m[0], ll = l[0];
-#pragma unroll
-    for (int h = 1; h < NQ; ++h)
-      if (lane == h) { mm = m[h]; ll = l[h]; }
-    wm[wv][lane] = mm;
-    wl[wv][lane] = ll;
-  }
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) *(float4*)&wo[wv][h][4 * lane] = o4[h];
-  __syncthreads();
-  const size_t pstride = (size_t)nq * (2 + kHeadDim);
-  float O[NQ];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) {
-    O[h] = 0.f;
-    if (h < nq) {
-      const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-      float L = 0.f, Ov = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
-        L = fmaf(f, wl[w][h], L);
-        Ov = fmaf(f, wo[w][h][tid], Ov);
-      }
-      O[h] = Ov;
-      if (tid == 0) { hstat[h][0] = M; hstat[h][1] = L; }
-    }
-  }
-  if (nch == 1) {   // a single chunk is the result
-    __syncthreads();
-    for (int h = 0; h < nq; ++h) attn_out[h * kHeadDim + tid] = O[h] / hstat[h][1];
-    return;
-  }
-  float* mypart = part + (size_t)b * pstride;
-  for (int h = 0; h < nq; ++h) st_dev(mypart + h * (2 + kHeadDim) + 2 + tid, O[h]);
-  __syncthreads();
-  if (tid < nq) {
-    st_dev(mypart + tid * (2 + kHeadDim), hstat[tid][0]);
-    st_dev(mypart + tid * (2 + kHeadDim) + 1, hstat[tid][1]);
-  }
-
-  // 4. the last block to finish merges every chunk. Partials are written
-  // through to the device coherence point and the counter is a device-scope
-  // atomic issued after all of this block's stores have completed.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (old == (unsigned int)(nch - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  // One device-scope acquire (an L2 invalidate, no write-back) makes the
-  // written-through partials of every block visible to ordinary loads.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  // chunk statistics -> LDS; every load is issued before any is used
-  const int nst = nch * nq;
-  for (int i0 = 0; i0 < nst; i0 += 256 * 4) {
-    float mv[4], lv[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = i0 + tid + 256 * k;
-      if (i < nst) {
-        const float* pp = part + (size_t)(i / nq) * pstride + (i % nq) * (2 + kHeadDim);
-        mv[k] = pp[0];
-        lv[k] = pp[1];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = i0 + tid + 256 * k;
-      if (i < nst) { sm[i] = mv[k]; sf[i] = lv[k]; }
-    }
-  }
-  __syncthreads();
-  // per head (wave h): max over the chunks, weights exp(m_c - M) into LDS,
-  // total L; lanes stride over the chunks, then a wave reduction
-  if (wv < nq) {
-    float M = -INFINITY;
-    for (int c = lane; c < nch; c += 64) M = fmaxf(M, sm[c * nq + wv]);
-    M = wave_max(M);
-    float L = 0.f;
-    for (int c = lane; c < nch; c += 64) {
-      const float f = expf(sm[c * nq + wv] - M);
-      sm[c * nq + wv] = f;
-      L = fmaf(f, sf[c * nq + wv], L);
-    }
-    L = wave_sum(L);
-    if (lane == 0) hstat[wv][1] = L;
-  }
-  __syncthreads();
-  float Lh[NQ];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) Lh[h] = h < nq ? hstat[h][1] : 1.f;
-  float acc[NQ];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) acc[h] = 0.f;
-  // branch-free: chunk indices are clamped to nch - 1 (always in bounds) and
-  // the weights of the clamped repeats are zero
-  for (int c0 = 0; c0 < nch; c0 += 16) {
-    float ov[16][NQ];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int cc = min(c0 + k, nch - 1);
-#pragma unroll
-      for (int h = 0; h < NQ; ++h) ov[k][h] = part[(size_t)cc * pstride + h * (2 + kHeadDim) + 2 + tid];
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int cc = min(c0 + k, nch - 1);
-#pragma unroll
-      for (int h = 0; h < NQ; ++h) {
-        const float w = (c0 + k < nch && h < nq) ? sm[cc * nq + min(h, nq - 1)] : 0.f;
-        acc[h] = fmaf(w, ov[k][h], acc[h]);
-      }
-    }
-  }
-  for (int h = 0; h < nq; ++h) attn_out[h * kHeadDim + tid] = acc[h] / Lh[h];
-  if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
 // Decode attention (one KV head, head_dim 256, up to 4 query heads), one
 // chunk of positions per block; the chunk partials (max, sum, o) go to
 // memory and the attention output projection merges them in its prologue
@@ -1342,6 +981,223 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 }
 
 // ---------------------------------------------------------------------------
+// Batched prefill attention (no reference counterpart: the reference attends
+// one prompt token per decode pass, engine.ts:923-928, with the
+// scores / softmax / weighted V of shaders.ts:229-325).
+//
+// Block (x = key chunk, y = query tile) covers 16 prompt rows; wave h
+// computes query head h of those rows over the chunk's keys, which are
+// staged 32 rows at a time in LDS and shared by the heads (one KV head).
+// Both products run on v_mfma_f32_16x16x4f32:
+//   S^T = K Q^T  A = 16 key rows, B = Q^T. In step (t, u) lane group
+//                g = lane / 16 supplies dim 16 t + 4 g + u of key / row
+//                lane % 16; afterwards lane l holds
+//                S^T[key 16 j + 4 g + r][row l % 16] for r < 4.
+//   O += P V     the k-index runs over (j, r) so that lane l's own S^T
+//                registers are its A operand (key 16 j + 4 g + r), B = V rows;
+//                lane l holds O[row 4 g + r][16 i + l % 16] for i < 16.
+// Softmax statistics of row l % 16 stay online per lane: the max is reduced
+// over the four lane groups each tile, the sum once at the end. LDS rows are
+// unpadded and XOR-swizzled so that K reads (ds_read_b128, 16 keys per lane
+// group) and V reads (ds_read_b32, 4 keys x 16 dims) hit distinct banks:
+// float4 slot f of K row k sits at slot f ^ (k % 16), column d of V row k
+// at d ^ 16 ((k / 4) % 4). A query tile whose span fits one chunk writes
+// O / l; otherwise every chunk leaves (m, l, O) in `part` for
+// k_attn_pf_merge.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kPfRows = 16;   // query rows per block (one MFMA tile)
+constexpr int kPfKeys = 32;   // keys per LDS tile
+
+__device__ __forceinline__ int pf_key_lo(const AttnArgs& a, int pos) {
+  return a.window > 0 ? max(0, pos - a.window + 1) : 0;
+}
+
+// Keys of query tile qt: [lo(first row), last row], chunks of pf_chunk keys.
+__device__ __forceinline__ void pf_tile_span(const AttnArgs& a, int qt, int* klo, int* khi, int* nkc) {
+  const int p_first = a.pf_start + qt * kPfRows;
+  const int p_last = a.pf_start + min(qt * kPfRows + kPfRows - 1, a.pf_rows - 1);
+  *klo = pf_key_lo(a, p_first);
+  *khi = p_last;
+  *nkc = (p_last - *klo + a.pf_chunk) / a.pf_chunk;
+}
+
+__global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
+  __shared__ __align__(16) float Ks[kPfKeys * kHeadDim];
+  __shared__ __align__(16) float Vs[kPfKeys * kHeadDim];
+  const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int M = a.pf_rows, nq = a.n_q, qt = blockIdx.y, kc = blockIdx.x;
+  int klo, khi, nkc;
+  pf_tile_span(a, qt, &klo, &khi, &nkc);
+  if (kc >= nkc) return;
+  const int k0 = klo + kc * a.pf_chunk, k1 = min(k0 + a.pf_chunk, khi + 1);
+  const bool active = h < nq;
+
+  // staging: wave w moves key rows 4 i + w of a tile, lane = float4 slot.
+  // V of a tile is fetched while its scores run, K of the next tile while
+  // the weighted sum runs, so 32 staging registers cover both.
+  float4 st[8];
+  auto fetch = [&](const float* cache, int kt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = kt + 4 * i + h;
+      st[i] = *(const float4*)(cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
+      if (key >= k1) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stage_k = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kr = 4 * i + h;
+      *(float4*)&Ks[kr * kHeadDim + 4 * (lane ^ (kr & 15))] = st[i];
+    }
+  };
+  auto stage_v = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kr = 4 * i + h;
+      *(float4*)&Vs[kr * kHeadDim + ((4 * lane) ^ (16 * ((kr >> 2) & 3)))] = st[i];
+    }
+  };
+  fetch(a.k_cache, k0);
+
+  // q (normed + roped) of row l % 16, dims 16 t + 4 g .. +3
+  const int row = qt * kPfRows + c16;
+  const bool row_ok = row < M;
+  const int prow = a.pf_start + row, plo = pf_key_lo(a, prow);
+  const float* qp = a.qkv + (size_t)min(row, M - 1) * (nq * kHeadDim + 2 * kHeadDim) + min(h, nq - 1) * kHeadDim + 4 * g;
+  float4 q[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) q[t] = *(const float4*)(qp + 16 * t);
+  stage_k();
+
+  f32x4 o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  for (int kt = k0; kt < k1; kt += kPfKeys) {
+    fetch(a.v_cache, kt);
+    __syncthreads();   // K of this tile staged; the previous tile's V reads done
+    float p[2][4];
+    float alpha = 1.f;
+    if (active) {
+      f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float4 kk = *(const float4*)&Ks[(16 * j + c16) * kHeadDim + 4 * ((4 * t + g) ^ c16)];
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, q[t].x, s[j], 0, 0, 0);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, q[t].y, s[j], 0, 0, 0);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, q[t].z, s[j], 0, 0, 0);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, q[t].w, s[j], 0, 0, 0);
+        }
+      }
+      // scale + causal / window mask; online softmax of row l % 16
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kt + 16 * j + 4 * g + r;
+          const bool ok = row_ok && key < k1 && key >= plo && key <= prow;
+          p[j][r] = ok ? s[j][r] * a.scale : -INFINITY;
+          mx = fmaxf(mx, p[j][r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m, mx);
+      const float mb = mn == -INFINITY ? 0.f : mn;   // a row with no key yet keeps p = 0
+      alpha = expf(m - mb);
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[j][r] = expf(p[j][r] - mb);
+          ps += p[j][r];
+        }
+      l = fmaf(l, alpha, ps);
+      m = mn;
+    }
+    __syncthreads();   // every K read of this tile done
+    stage_v();
+    if (kt + kPfKeys < k1) fetch(a.k_cache, kt + kPfKeys);
+    __syncthreads();   // V of this tile staged
+    if (active) {
+      // O rows 4 g + r take the factors of the lanes that hold those rows
+      float ar[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[i][r] *= ar[r];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float* vr = &Vs[(16 * j + 4 * g + r) * kHeadDim + c16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j][r], vr[16 * (i ^ g)], o[i], 0, 0, 0);
+        }
+    }
+    if (kt + kPfKeys < k1) stage_k();   // no K reads until the next barrier
+  }
+  if (!active) return;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  float lr[4], mr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lr[r] = __shfl(l, 4 * g + r, 64);
+    mr[r] = __shfl(m, 4 * g + r, 64);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int orow = qt * kPfRows + 4 * g + r;
+    if (orow >= M) continue;
+    if (nkc == 1) {
+      float* out = a.attn_out + (size_t)orow * nq * kHeadDim + h * kHeadDim + c16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) out[16 * i] = o[i][r] / lr[r];
+    } else {
+      float* pp = a.part + (((size_t)orow * kPrefillChunks + kc) * nq + h) * (2 + kHeadDim);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pp[2 + 16 * i + c16] = o[i][r];
+      if (c16 == 0) {
+        pp[0] = mr[r];
+        pp[1] = lr[r];
+      }
+    }
+  }
+}
+
+// Rows of query tiles with more than one chunk: softmax-weighted sum of the
+// chunks' (m, l, O), one block per row, thread = head dim.
+__global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
+  const int row = blockIdx.x, tid = threadIdx.x, nq = a.n_q;
+  int klo, khi, nkc;
+  pf_tile_span(a, row / kPfRows, &klo, &khi, &nkc);
+  if (nkc == 1) return;
+  const float* pr = a.part + (size_t)row * kPrefillChunks * nq * (2 + kHeadDim);
+  for (int h = 0; h < nq; ++h) {
+    float M = -INFINITY;
+    for (int c = 0; c < nkc; ++c) M = fmaxf(M, pr[(c * nq + h) * (2 + kHeadDim)]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < nkc; ++c) {
+      const float* pc = pr + (c * nq + h) * (2 + kHeadDim);
+      const float f = pc[0] == -INFINITY ? 0.f : expf(pc[0] - M);
+      L = fmaf(f, pc[1], L);
+      O = fmaf(f, pc[2 + tid], O);
+    }
+    a.attn_out[(size_t)row * nq * kHeadDim + h * kHeadDim + tid] = O / L;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Batched prefill (no reference counterpart: the reference runs the decode
 // pass once per prompt token, engine.ts:923-928).
 //
@@ -1352,7 +1208,6 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // sub-tile (2 x 4 MFMA tiles). Next stage's global loads are issued before
 // the current stage's MFMAs.
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kGBM = 64, kGBN = 128, kGStr = 68;
 
 template <int EPI>
@@ -1510,25 +1365,34 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
   row_norm_out(v, a.w_pre, H, a.eps, a.x_out + o, sh4, n);
 }
 
-// k of each prompt row: per-head RMSNorm + NEOX RoPE, then k and v into the
-// cache at pf_start + row (fusedPerHeadNormRope + kvCacheStore).
+// One block per prompt row: RMSNorm + NEOX RoPE of the key head (into the
+// cache, with v) and of every query head, the latter in place in the QKV
+// rows for the attention kernel (fusedPerHeadNormRope, shaders.ts:420-467).
 __global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
   __shared__ float sh4[4];
   __shared__ float kk[kHeadDim];
   const int row = blockIdx.x, tid = threadIdx.x;
   const int pos = a.pf_start + row;
-  const float* q = a.qkv + (size_t)row * (a.n_q * kHeadDim + 2 * kHeadDim) + a.n_q * kHeadDim;
+  float* qrow = const_cast<float*>(a.qkv) + (size_t)row * (a.n_q * kHeadDim + 2 * kHeadDim);
+  const float* q = qrow + a.n_q * kHeadDim;
   const float k = q[tid], v = q[kHeadDim + tid], w = a.k_norm[tid];
   const float* rt = a.rope + (size_t)pos * kHeadDim;
   const float cs = rt[tid & 127], sn = rt[128 + (tid & 127)];
-  const float rms = sqrtf(block_sum256(k * k, sh4) / (float)kHeadDim + a.eps);
-  kk[tid] = (k * w) / rms;
-  __syncthreads();
-  float out;
-  if (tid < 128) out = kk[tid] * cs - kk[tid + 128] * sn;
-  else out = kk[tid - 128] * sn + kk[tid] * cs;
-  a.k_cache[(size_t)pos * kHeadDim + tid] = out;
+  auto norm_rope = [&](float x, float wt) {
+    const float rms = sqrtf(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
+    kk[tid] = (x * wt) / rms;
+    __syncthreads();
+    const float out = tid < 128 ? kk[tid] * cs - kk[tid + 128] * sn : kk[tid - 128] * sn + kk[tid] * cs;
+    __syncthreads();
+    return out;
+  };
+  a.k_cache[(size_t)pos * kHeadDim + tid] = norm_rope(k, w);
   a.v_cache[(size_t)pos * kHeadDim + tid] = v;
+  const float wq = a.q_norm[tid];
+  for (int h = 0; h < a.n_q; ++h) {
+    const float x = qrow[h * kHeadDim + tid];
+    qrow[h * kHeadDim + tid] = norm_rope(x, wq);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1695,8 +1559,14 @@ int launch_attention(const AttnArgs& a, int grid, void* stream) {
 }
 
 int launch_prefill_attention(const AttnArgs& a, int M, void* stream) {
-  if (a.n_q < 1 || a.n_q > kAttnMaxQ || M < 1 || a.max_chunks != kPrefillChunks) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn<true>, dim3(kPrefillChunks, M), dim3(256), 0, (hipStream_t)stream, a);
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || M < 1 || a.pf_rows != M || a.pf_start < 0 || a.window < 0 ||
+      a.pf_chunk < kPfKeys || a.pf_chunk % kPfKeys)
+    return (int)hipErrorInvalidValue;
+  const int span = prefill_max_span(a.window, a.pf_start, M);
+  const int nkc = (span + a.pf_chunk - 1) / a.pf_chunk;
+  if (nkc > kPrefillChunks) return (int)hipErrorInvalidValue;   // `part` holds kPrefillChunks per row
+  hipLaunchKernelGGL(k_attn_pf, dim3(nkc, (M + kPfRows - 1) / kPfRows), dim3(256), 0, (hipStream_t)stream, a);
+  if (nkc > 1) hipLaunchKernelGGL(k_attn_pf_merge, dim3(M), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

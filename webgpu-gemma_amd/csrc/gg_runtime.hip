@@ -92,7 +92,6 @@ struct gg_ctx {
   float *rope_local = nullptr, *rope_global = nullptr;   // [ctx][cos|sin][128]
   float* cand_val = nullptr;
   uint32_t *cand_id = nullptr, *top = nullptr, *seen = nullptr;
-  unsigned int* counters = nullptr;   // attention chunk arrivals
   DevState* st = nullptr;
   int32_t* tokens = nullptr;
   int32_t* d_ids = nullptr;           // staging for gg_penalty_add
@@ -104,7 +103,6 @@ struct gg_ctx {
   int pf_M = 0;
   float *pf_hidden = nullptr, *pf_residual = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
   float *pf_o = nullptr, *pf_act = nullptr, *pf_part = nullptr;
-  unsigned int* pf_counters = nullptr;
 
   // pinned host mirrors
   DevState* h_st = nullptr;
@@ -248,7 +246,6 @@ int record_forward(gg_ctx* c) {
     at.st = c->st;
     at.part = c->attn_part;
     at.attn_out = c->attn_out;
-    at.max_chunks = kDecMaxChunks;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
       ProbeScope ps(c, GG_PROBE_ATTN, l);
@@ -405,6 +402,7 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     kv.pf_start = start;
     kv.qkv = c->pf_qkv;
     kv.n_q = c->NQ;
+    kv.q_norm = Ly.norm[N_QN];
     kv.k_norm = Ly.norm[N_KN];
     kv.rope = swa ? c->rope_local : c->rope_global;
     kv.k_cache = Ly.kc;
@@ -413,19 +411,15 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     AttnArgs at{};
     at.qkv = c->pf_qkv;
     at.n_q = c->NQ;
-    at.q_norm = Ly.norm[N_QN];
-    at.k_norm = Ly.norm[N_KN];
-    at.rope = kv.rope;
     at.k_cache = Ly.kc;
     at.v_cache = Ly.vc;
     at.window = swa ? c->c.sliding_window : 0;
-    at.eps = eps;
     at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
     at.part = c->pf_part;
-    at.counter = c->pf_counters;
     at.attn_out = c->pf_attn;
     at.pf_start = start;
-    at.max_chunks = kPrefillChunks;
+    at.pf_rows = M;
+    at.pf_chunk = prefill_chunk(at.window, start, M);
     GG_TRY(launch_rc(c, launch_prefill_attention(at, M, s), "prefill attention"));
     GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_attn, Ly.o, c->lay_o, M, c->pf_o), s), "prefill o"));
     RowArgs r1 = r;
@@ -476,7 +470,7 @@ gg_ctx* gg_create(const gg_config* cfg) {
   if (k.head_dim != kHeadDim || k.num_kv_heads != 1 || k.num_q_heads < 1 || k.num_q_heads > kAttnMaxQ ||
       k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > 2048 || k.intermediate_size <= 0 ||
       k.intermediate_size % 64 || k.intermediate_size > kMaxK || k.vocab_size <= 0 || k.vocab_size % 64 ||
-      k.num_layers <= 0 || k.context_length <= 0 || k.context_length > 32 * kAttnMaxChunks * 8 ||
+      k.num_layers <= 0 || k.context_length <= 0 || k.context_length > kMaxContext ||
       k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK) {
     set_err(nullptr, GG_ERR_INVALID,
             "unsupported config: needs head_dim 256, one KV head, <= 4 query heads, hidden/intermediate/vocab "
@@ -675,11 +669,9 @@ int gg_finalize(gg_ctx* c) {
   GG_TRY(dalloc(c, &c->top, 512 * 4));
   GG_TRY(dalloc(c, &c->seen, (size_t)cdiv(c->V, 32) * 4));
   GG_TRY(dalloc(c, &c->st, sizeof(DevState)));
-  GG_TRY(dalloc(c, &c->counters, 256));
   GG_TRY(dalloc(c, &c->tokens, (size_t)c->CTX * 4));
   GG_TRY(dalloc(c, &c->d_ids, (size_t)c->CTX * 4));
   GG_HIP(c, hipMemset(c->st, 0, sizeof(DevState)));
-  GG_HIP(c, hipMemset(c->counters, 0, 256));
   if (c->c.prefill_batch > 0) {
     const int M = std::min(c->c.prefill_batch, c->CTX);
     c->pf_M = M;
@@ -692,8 +684,6 @@ int gg_finalize(gg_ctx* c) {
     GG_TRY(dalloc(c, &c->pf_attn, (size_t)M * c->QD * 4));
     GG_TRY(dalloc(c, &c->pf_act, (size_t)M * c->I * 4));
     GG_TRY(dalloc(c, &c->pf_part, (size_t)M * kPrefillChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
-    GG_TRY(dalloc(c, &c->pf_counters, (size_t)M * 4));
-    GG_HIP(c, hipMemset(c->pf_counters, 0, (size_t)M * 4));
   }
   GG_HIP(c, hipMemset(c->seen, 0, (size_t)cdiv(c->V, 32) * 4));
   GG_HIP(c, hipMemset(c->tokens, 0, (size_t)c->CTX * 4));
