@@ -122,7 +122,8 @@ struct AttnArgs {
   const DevState* st;
   float* part;             // decode: o [kDecMaxChunks][kAttnMaxQ][256] then (m, l) [kDecMaxChunks][kAttnMaxQ][2];
                            // batched prefill: (m, l, o[256]) [row][kPrefillChunks][n_q]
-  float* attn_out;         // decode [n_q * 256]; batched prefill [row][n_q * 256]
+  float* attn_out;         // decode [n_q * 256]
+  uint16_t* pf_out;        // batched prefill: hi plane [row][n_q * 256], then lo plane
   float* q_dbg;            // decode, optional: normed+roped q of this token
   // batched prefill: prompt row r sits at position pf_start + r; q of every
   // row is already normed + roped in `qkv`, K/V of every position are in the
@@ -132,12 +133,18 @@ struct AttnArgs {
   int pf_chunk;
 };
 
-// Prefill GEMM: C[M x N] = A[M x K] * W[N x K]^T, W item-planar (GR = 8 or 32).
+// Prefill GEMM on bf16 MFMA: C[M x N] = A[M x K] * W[N x K]^T. A comes as two
+// bf16 planes (hi = bf16(x), lo = bf16(x - hi)); W as its int8 values in
+// bf16 (exact) with the fp32 scale of every 32-wide block, applied to each
+// block's MFMA partial in fp32.
 struct GemmArgs {
-  const float* A;          // [M][K] row-major activations
-  const uint8_t* W;
-  int M, N, K, Kp, KpS, GR;
-  float* C;                // [M][N] (EPI_OUT) or act [M][N/2] (EPI_GEGLU)
+  const uint16_t* A;       // hi plane [M][K], then lo plane [M][K]
+  const uint16_t* W;       // [N][K]
+  const float* D;          // [N][K / 32]
+  int M, N, K;
+  float* C;                // EPI_OUT: [M][N]
+  uint16_t* act;           // EPI_GEGLU: hi plane [M][N/2], then lo plane; gate / up rows
+                           // alternate in groups of 16 (16 gate rows, then their up rows)
 };
 
 // Row-wise prefill helpers: one block per prompt row.
@@ -154,7 +161,7 @@ struct RowArgs {
   const float* w_post;
   const float* w_pre;
   float* res_out;          // [M][H] new residual stream
-  float* x_out;            // [M][H] normed GEMM input
+  uint16_t* x_out;         // normed GEMM input: hi plane [M][H], then lo plane
   float* last_hidden;      // optional: row M-1 of res_out (per-layer history)
   // KV: k/v of each row into the cache, q heads normed + roped in place
   const float* qkv;
@@ -203,6 +210,10 @@ int launch_select(const SelectArgs& a, void* stream);
 int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,
                   long long dst_row_offset, int interleave_half, void* stream);
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
+// GGUF Q8_0 rows -> prefill GEMM weights: source row r to row r + off, or
+// with half = 16 to (r / 16) * 32 + r % 16 + off (gate: off 0, up: off 16).
+int launch_q8_bf16(const uint8_t* src, uint16_t* wb, float* wd, long long rows, int K, long long off, int half,
+                   void* stream);
 int launch_seen_add(uint32_t* seen, DevState* st, const int32_t* ids, int n, int V, void* stream);
 int launch_prefill_attention(const AttnArgs& a, int M, void* stream);
 int launch_gemm(int epi, const GemmArgs& a, void* stream);

@@ -1006,6 +1006,15 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // k_attn_pf_merge.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// x = hi + lo + e with hi = bf16(x), lo = bf16(x - hi), |e| <= 2^-17 |x|
+// (the input format of the prefill GEMMs).
+__device__ __forceinline__ void split_bf16(float x, uint16_t* hi, uint16_t* lo) {
+  const __bf16 h = (__bf16)x;
+  *hi = __builtin_bit_cast(uint16_t, h);
+  *lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
+}
+
 constexpr int kPfRows = 16;   // query rows per block (one MFMA tile)
 constexpr int kPfKeys = 32;   // keys per LDS tile
 
@@ -1160,9 +1169,10 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
     const int orow = qt * kPfRows + 4 * g + r;
     if (orow >= M) continue;
     if (nkc == 1) {
-      float* out = a.attn_out + (size_t)orow * nq * kHeadDim + h * kHeadDim + c16;
+      uint16_t* out = a.pf_out + (size_t)orow * nq * kHeadDim + h * kHeadDim + c16;
+      const size_t plane = (size_t)M * nq * kHeadDim;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) out[16 * i] = o[i][r] / lr[r];
+      for (int i = 0; i < 16; ++i) split_bf16(o[i][r] / lr[r], &out[16 * i], &out[plane + 16 * i]);
     } else {
       float* pp = a.part + (((size_t)orow * kPrefillChunks + kc) * nq + h) * (2 + kHeadDim);
 #pragma unroll
@@ -1193,121 +1203,140 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
       L = fmaf(f, pc[1], L);
       O = fmaf(f, pc[2 + tid], O);
     }
-    a.attn_out[(size_t)row * nq * kHeadDim + h * kHeadDim + tid] = O / L;
+    const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + tid;
+    split_bf16(O / L, &a.pf_out[e], &a.pf_out[(size_t)a.pf_rows * nq * kHeadDim + e]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Batched prefill (no reference counterpart: the reference runs the decode
-// pass once per prompt token, engine.ts:923-928).
+// Batched prefill GEMMs (no reference counterpart: the reference runs the
+// decode pass once per prompt token, engine.ts:923-928).
 //
-// k_gemm: C[M x N] = A[M x K] * W[N x K]^T on fp32 MFMA (v_mfma_f32_16x16x4f32)
-// with W's Q8_0 pairs dequantised exactly (q * d is exact in f32) into LDS,
-// so the products match the decode GEMV's up to summation order. Block tile
-// 64 (rows) x 128 (features) x 64 (one pair column); wave w owns a 32 x 64
-// sub-tile (2 x 4 MFMA tiles). Next stage's global loads are issued before
-// the current stage's MFMAs.
+// k_gemm: C[M x N] = A[M x K] * W[N x K]^T on bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16, K = 32 = one Q8_0 block). W holds the int8
+// weights as bf16 (exact); A is split by its producer into hi = bf16(x) and
+// lo = bf16(x - hi), so x - hi - lo is within 2^-17 |x| and every product
+// q * hi, q * lo is exact in the fp32 accumulator. Per 32-block the two
+// MFMAs give sum_j q_j x_j, which is scaled by the block's fp32 scale d and
+// added to the output in fp32 -- the linearQ8 structure (shaders.ts:123-142)
+// with the block sum on the matrix cores.
+//
+// Block tile 128 (rows) x 128 (features) x 64 (k step), four waves of 64 x 64
+// (4 x 4 MFMA tiles). LDS rows are padded to 72 bf16 so that the 16 lanes of
+// a lane group (16 rows, one 16-byte chunk) cover all banks; the next step's
+// global loads are issued before the current step's MFMAs.
 // ---------------------------------------------------------------------------
-constexpr int kGBM = 64, kGBN = 128, kGStr = 68;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kGBM = 128, kGBN = 128, kGBP = 72;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
+}
 
 template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-  __shared__ float As[kGBM][kGStr];
-  __shared__ float Bs[kGBN][kGStr];
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint16_t Ah[kGBM * kGBP];
+  __shared__ __align__(16) uint16_t Al[kGBM * kGBP];
+  __shared__ __align__(16) uint16_t Ws[kGBN * kGBP];
+  __shared__ float Ds[kGBN * 2];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int M = a.M, K = a.K;
   const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
-  const int wm = (wv >> 1) * 32, wn = (wv & 1) * 64;
-  // A loader: row tid/4, 16 k at (tid%4)*16; W loader (tid < 128): row n0+tid
-  const int ar = tid >> 2, ak = (tid & 3) * 16;
-  const float* arow = a.A + (size_t)min(m0 + ar, a.M - 1) * a.K + ak;
-  const int wn_row = n0 + (tid & 127);
-  // pair (row wn_row, column c): item (wn_row / GR) * KpS + c / CI, slot (c % CI) * GR + wn_row % GR
-  const int GR = a.GR, CI = 64 / GR;
-  const uint8_t* wbase = a.W + (size_t)(wn_row / GR) * a.KpS * kColBytes;
-  auto wload = [&](int c, Pair& P) {
-    load_planes(wbase + (size_t)(c / CI) * kColBytes, (c % CI) * GR + wn_row % GR, P);
+  const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
+  const size_t MK = (size_t)M * K;
+  // staging: rows tid / 8 + 32 i, 16-byte chunk tid % 8 of the 64-wide step;
+  // scale (row tid / 2, block tid % 2)
+  const int sr = tid >> 3, sc = (tid & 7) * 8;
+  const uint16_t* a0 = a.A + sc;
+  const uint16_t* w0 = a.W + (size_t)(n0 + sr) * K + sc;
+  const float* dp = a.D + (size_t)(n0 + (tid >> 1)) * (K / 32) + (tid & 1);
+  u32x4 rh[4], rl[4], rw[4];
+  float rd;
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t* ar = a0 + (size_t)min(m0 + sr + 32 * i, M - 1) * K + k0;
+      rh[i] = *(const u32x4*)ar;
+      rl[i] = *(const u32x4*)(ar + MK);
+      rw[i] = *(const u32x4*)(w0 + (size_t)(32 * i) * K + k0);
+    }
+    rd = dp[k0 / 32];
+  };
+  auto stage = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (sr + 32 * i) * kGBP + sc;
+      *(u32x4*)&Ah[r] = rh[i];
+      *(u32x4*)&Al[r] = rl[i];
+      *(u32x4*)&Ws[r] = rw[i];
+    }
+    Ds[tid] = rd;
   };
 
-  f32x4 acc[2][4];
+  f32x4 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  float4 av[4];
-  Pair wp;
+  fetch(0);
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    __syncthreads();   // the previous step's LDS reads are done
+    stage();
+    __syncthreads();
+    if (k0 + 64 < K) fetch(k0 + 64);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + 4 * q);
-  if (tid < 128) wload(0, wp);
-
-  for (int c = 0; c < a.Kp; ++c) {
+    for (int b = 0; b < 2; ++b) {
+      bf16x8 xh[4], xl[4], w[4];
+      float d[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) *(float4*)&As[ar][ak + 4 * q] = av[q];
-    if (tid < 128) {
-      const float d0 = f16_lo(wp.w[0]), d1 = f16_hi(wp.w[8]);
-      float* br = Bs[tid];
-#pragma unroll
-      for (int j = 0; j < 32; j += 4) {
-        float4 v0, v1;
-        v0.x = sbyte(wp.w[(2 + j) >> 2], (2 + j) & 3) * d0;
-        v0.y = sbyte(wp.w[(3 + j) >> 2], (3 + j) & 3) * d0;
-        v0.z = sbyte(wp.w[(4 + j) >> 2], (4 + j) & 3) * d0;
-        v0.w = sbyte(wp.w[(5 + j) >> 2], (5 + j) & 3) * d0;
-        v1.x = sbyte(wp.w[9 + (j >> 2)], 0) * d1;
-        v1.y = sbyte(wp.w[9 + (j >> 2)], 1) * d1;
-        v1.z = sbyte(wp.w[9 + (j >> 2)], 2) * d1;
-        v1.w = sbyte(wp.w[9 + (j >> 2)], 3) * d1;
-        *(float4*)&br[j] = v0;
-        *(float4*)&br[32 + j] = v1;
+      for (int i = 0; i < 4; ++i) {
+        const int o = (wm + 16 * i + c16) * kGBP + 32 * b + 8 * g;
+        xh[i] = lds_bf16x8(&Ah[o]);
+        xl[i] = lds_bf16x8(&Al[o]);
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w[j] = lds_bf16x8(&Ws[(wn + 16 * j + c16) * kGBP + 32 * b + 8 * g]);
+        d[j] = Ds[(wn + 16 * j + c16) * 2 + b];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh[i], w[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl[i], w[j], p, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(d[j], p[r], acc[i][j][r]);
+        }
     }
-    __syncthreads();
-    if (c + 1 < a.Kp) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) av[q] = *(const float4*)(arow + (size_t)(c + 1) * 64 + 4 * q);
-      if (tid < 128) wload(c + 1, wp);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 64; kk += 4) {
-      float af[2], bf[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = As[wm + i * 16 + (lane & 15)][kk + (lane >> 4)];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = Bs[wn + j * 16 + (lane & 15)][kk + (lane >> 4)];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
   }
   // D[i][j] of a 16x16 tile: lane l, register r -> row 4 (l / 16) + r, col l % 16
+  const size_t half_plane = (size_t)M * (a.N / 2);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + wm + 16 * i + 4 * g + r;
+      if (m >= M) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + i * 16 + 4 * (lane >> 4) + r;
-        const int n = n0 + wn + j * 16 + (lane & 15);
-        const float v = acc[i][j][r];
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn + 16 * j + c16;
         if (EPI == EPI_OUT) {
-          if (m < a.M) a.C[(size_t)m * a.N + n] = v;
-        } else if (a.GR == 8) {
-          // fused gate/up rows: 4 gate rows then their 4 up rows per group of 8
-          const float up = __shfl(v, lane + 4, 64);
-          if (m < a.M && (n & 4) == 0) a.C[(size_t)m * (a.N / 2) + (n >> 3) * 4 + (n & 3)] = gelu_mul(v, up);
+          a.C[(size_t)m * a.N + n] = acc[i][j][r];
         } else if ((j & 1) == 0) {
-          // groups of 32: 16 gate rows (tile j) then their 16 up rows (tile j + 1)
-          const float up = acc[i][(j + 1) & 3][r];
-          if (m < a.M) a.C[(size_t)m * (a.N / 2) + (n >> 5) * 16 + (n & 15)] = gelu_mul(v, up);
+          // 16 gate rows (tile j), then their 16 up rows (tile j + 1)
+          const size_t o = (size_t)m * (a.N / 2) + (n >> 5) * 16 + (n & 15);
+          split_bf16(gelu_mul(acc[i][j][r], acc[i][j | 1][r]), &a.act[o], &a.act[half_plane + o]);
         }
       }
+    }
 }
 
 // Row kernels (one block per prompt row, H <= 2048).
-__device__ __forceinline__ void row_norm_out(const float* r, const float* w, int H, float eps, float* out,
-                                             float* sh4, int n) {
+__device__ __forceinline__ void row_norm_out(const float* r, const float* w, int H, float eps, uint16_t* out,
+                                             size_t plane, float* sh4, int n) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -1315,7 +1344,10 @@ __device__ __forceinline__ void row_norm_out(const float* r, const float* w, int
   const float rms = sqrtf(block_sum256(ss, sh4) / (float)H + eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    if (i < n) out[threadIdx.x + 256 * i] = (r[i] * w[threadIdx.x + 256 * i]) / rms;
+    if (i < n) {
+      const int e = threadIdx.x + 256 * i;
+      split_bf16((r[i] * w[e]) / rms, &out[e], &out[plane + e]);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_rows_embed(RowArgs a) {
@@ -1334,7 +1366,7 @@ __global__ __launch_bounds__(256) void k_rows_embed(RowArgs a) {
       h[i] = embed_elem(g, token, tid + 256 * i);
       a.res_out[(size_t)row * H + tid + 256 * i] = h[i];
     }
-  row_norm_out(h, a.w_pre, H, a.eps, a.x_out + (size_t)row * H, sh4, n);
+  row_norm_out(h, a.w_pre, H, a.eps, a.x_out + (size_t)row * H, (size_t)a.M * H, sh4, n);
 }
 
 __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
@@ -1362,7 +1394,7 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
       a.res_out[o + tid + 256 * i] = v[i];
       if (a.last_hidden && row == a.M - 1) a.last_hidden[tid + 256 * i] = v[i];
     }
-  row_norm_out(v, a.w_pre, H, a.eps, a.x_out + o, sh4, n);
+  row_norm_out(v, a.w_pre, H, a.eps, a.x_out + o, (size_t)a.M * H, sh4, n);
 }
 
 // One block per prompt row: RMSNorm + NEOX RoPE of the key head (into the
@@ -1429,6 +1461,29 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
   const uint16_t sb = (uint16_t)(blk[0] | (blk[1] << 8));
   const float scale = (float)__builtin_bit_cast(_Float16, sb);
   out[i] = (float)(int8_t)blk[2 + (i & 31)] * scale;
+}
+
+// GGUF Q8_0 rows -> the prefill GEMM's weights: int8 values as bf16 (exact)
+// and fp32 block scales, one thread per 32-block. Source row r goes to row
+// r + off, or with half = 16 to (r / 16) * 32 + r % 16 + off (gate / up
+// groups of 16 + 16 rows).
+__global__ __launch_bounds__(256) void k_q8_bf16(const uint8_t* __restrict__ src, uint16_t* __restrict__ wb,
+                                                 float* __restrict__ wd, long long rows, int K, long long off,
+                                                 int half) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int nb = K / 32;
+  if (idx >= rows * nb) return;
+  const long long r = idx / nb;
+  const int b = (int)(idx - r * nb);
+  const long long R = half > 0 ? (r / half) * 2 * half + r % half + off : r + off;
+  const uint8_t* blk = src + (size_t)idx * 34;
+  wd[R * nb + b] = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8)));
+  uint32_t* o = (uint32_t*)(wb + R * K + 32 * b);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float f0 = (float)(int8_t)blk[2 + 2 * j], f1 = (float)(int8_t)blk[3 + 2 * j];
+    o[j] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+  }
 }
 
 // Add ids to the repetition-penalty bitmap (the turn's prompt tokens).
@@ -1595,6 +1650,16 @@ int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long
   return (int)hipGetLastError();
 }
 
+int launch_q8_bf16(const uint8_t* src, uint16_t* wb, float* wd, long long rows, int K, long long off, int half,
+                   void* stream) {
+  if (K % 32 || off < 0 || (half != 0 && half != 16)) return (int)hipErrorInvalidValue;
+  const long long total = rows * (K / 32);
+  if (total <= 0) return 0;
+  hipLaunchKernelGGL(k_q8_bf16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src, wb,
+                     wd, rows, K, off, half);
+  return (int)hipGetLastError();
+}
+
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
   if (n <= 0) return 0;
   hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src, out,
@@ -1603,8 +1668,8 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
 }
 
 int launch_gemm(int epi, const GemmArgs& a, void* stream) {
-  if (a.M < 1 || a.N % kGBN || a.K != a.Kp * 64 || (a.GR != 8 && a.GR != 32) ||
-      a.KpS != (a.Kp + 64 / a.GR - 1) / (64 / a.GR))
+  if (a.M < 1 || a.N < kGBN || a.N % kGBN || a.K < 64 || a.K % 64 || !a.A || !a.W || !a.D ||
+      (epi == EPI_OUT ? !a.C : !a.act))
     return (int)hipErrorInvalidValue;
   dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM);
   if (epi == EPI_OUT) hipLaunchKernelGGL(k_gemm<EPI_OUT>, grid, dim3(256), 0, (hipStream_t)stream, a);

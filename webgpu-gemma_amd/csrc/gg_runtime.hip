@@ -37,6 +37,10 @@ struct Layer {
   uint8_t* o = nullptr;
   uint8_t* gu = nullptr;    // gate/up rows interleaved GR/2 + GR/2 per row group
   uint8_t* down = nullptr;
+  // batched prefill GEMM weights (prefill_batch > 0): int8 values as bf16
+  // [N][K] and fp32 block scales [N][K / 32]; gate / up in groups of 16 + 16
+  uint16_t *qkv_b = nullptr, *o_b = nullptr, *gu_b = nullptr, *down_b = nullptr;
+  float *qkv_d = nullptr, *o_d = nullptr, *gu_d = nullptr, *down_d = nullptr;
   float* norm[N_NNORM] = {};
   float* kc = nullptr;
   float* vc = nullptr;
@@ -101,8 +105,9 @@ struct gg_ctx {
 
   // batched prefill (prefill_batch > 0)
   int pf_M = 0;
-  float *pf_hidden = nullptr, *pf_residual = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr;
-  float *pf_o = nullptr, *pf_act = nullptr, *pf_part = nullptr;
+  float *pf_hidden = nullptr, *pf_residual = nullptr, *pf_qkv = nullptr, *pf_o = nullptr, *pf_part = nullptr;
+  // GEMM inputs as bf16 hi / lo planes (the slice's M rows each)
+  uint16_t *pf_xn = nullptr, *pf_attn = nullptr, *pf_act = nullptr;
 
   // pinned host mirrors
   DevState* h_st = nullptr;
@@ -359,17 +364,17 @@ int sync(gg_ctx* c, const char* what) {
 }
 
 
-GemmArgs gemm_base(const float* A, const uint8_t* W, const Q8Layout& L, int M, float* C) {
+GemmArgs gemm_base(const uint16_t* A, const uint16_t* W, const float* D, int N, int K, int M, float* C,
+                   uint16_t* act) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
+  g.D = D;
   g.M = M;
-  g.N = L.rows;
-  g.K = L.K;
-  g.Kp = L.Kp;
-  g.KpS = L.KpS;
-  g.GR = L.GR;
+  g.N = N;
+  g.K = K;
   g.C = C;
+  g.act = act;
   return g;
 }
 
@@ -395,7 +400,7 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
   for (int l = 0; l < c->L; ++l) {
     Layer& Ly = c->layers[l];
     const bool swa = is_swa(c->c, l);
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_xn, Ly.qkv, c->lay_qkv, M, c->pf_qkv), s), "prefill qkv"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_xn, Ly.qkv_b, Ly.qkv_d, c->NQKV, c->H, M, c->pf_qkv, nullptr), s), "prefill qkv"));
     RowArgs kv{};
     kv.M = M;
     kv.eps = eps;
@@ -416,12 +421,12 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     at.window = swa ? c->c.sliding_window : 0;
     at.scale = (float)(1.0 / std::sqrt((double)kHeadDim));
     at.part = c->pf_part;
-    at.attn_out = c->pf_attn;
+    at.pf_out = c->pf_attn;
     at.pf_start = start;
     at.pf_rows = M;
     at.pf_chunk = prefill_chunk(at.window, start, M);
     GG_TRY(launch_rc(c, launch_prefill_attention(at, M, s), "prefill attention"));
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_attn, Ly.o, c->lay_o, M, c->pf_o), s), "prefill o"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_attn, Ly.o_b, Ly.o_d, c->H, c->QD, M, c->pf_o, nullptr), s), "prefill o"));
     RowArgs r1 = r;
     r1.pre = c->pf_o;
     r1.res = c->pf_hidden;
@@ -430,8 +435,8 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     r1.res_out = c->pf_residual;
     r1.x_out = c->pf_xn;
     GG_TRY(launch_rc(c, launch_rows_resid(r1, s), "prefill post-attn"));
-    GG_TRY(launch_rc(c, launch_gemm(EPI_GEGLU, gemm_base(c->pf_xn, Ly.gu, c->lay_gu, M, c->pf_act), s), "prefill gate/up"));
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_act, Ly.down, c->lay_down, M, c->pf_o), s), "prefill down"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_GEGLU, gemm_base(c->pf_xn, Ly.gu_b, Ly.gu_d, 2 * c->I, c->H, M, nullptr, c->pf_act), s), "prefill gate/up"));
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_act, Ly.down_b, Ly.down_d, c->H, c->I, M, c->pf_o, nullptr), s), "prefill down"));
     if (l + 1 < c->L) {
       RowArgs r2 = r;
       r2.pre = c->pf_o;
@@ -471,10 +476,12 @@ gg_ctx* gg_create(const gg_config* cfg) {
       k.hidden_size <= 0 || k.hidden_size % 64 || k.hidden_size > 2048 || k.intermediate_size <= 0 ||
       k.intermediate_size % 64 || k.intermediate_size > kMaxK || k.vocab_size <= 0 || k.vocab_size % 64 ||
       k.num_layers <= 0 || k.context_length <= 0 || k.context_length > kMaxContext ||
-      k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK) {
+      k.swa_period <= 0 || k.sliding_window < 0 || k.num_q_heads * kHeadDim > kMaxK ||
+      k.prefill_batch < 0 || (k.prefill_batch > 0 && k.hidden_size % 128)) {
     set_err(nullptr, GG_ERR_INVALID,
             "unsupported config: needs head_dim 256, one KV head, <= 4 query heads, hidden/intermediate/vocab "
-            "multiples of 64 (hidden <= 2048, intermediate <= 8192), context <= 65536");
+            "multiples of 64 (hidden <= 2048, intermediate <= 8192), context <= 65536, and for a batched "
+            "prefill a hidden size that is a multiple of 128");
     return nullptr;
   }
   int ndev = 0;
@@ -526,6 +533,14 @@ gg_ctx* gg_create(const gg_config* cfg) {
     for (int j = 0; j < N_NNORM; ++j) {
       const int n = (j == N_QN || j == N_KN) ? kHeadDim : c->H;
       if (dalloc(c, &Ly.norm[j], (size_t)n * 4)) return fail(0);
+    }
+    if (c->c.prefill_batch > 0) {
+      auto wcopy = [&](uint16_t** wb, float** wd, long long rows, long long K) {
+        return dalloc(c, wb, (size_t)(rows * K * 2)) || dalloc(c, wd, (size_t)(rows * (K / 32) * 4));
+      };
+      if (wcopy(&Ly.qkv_b, &Ly.qkv_d, c->NQKV, c->H) || wcopy(&Ly.o_b, &Ly.o_d, c->H, c->QD) ||
+          wcopy(&Ly.gu_b, &Ly.gu_d, 2LL * c->I, c->H) || wcopy(&Ly.down_b, &Ly.down_d, c->H, c->I))
+        return fail(0);
     }
   }
   return c;
@@ -623,6 +638,22 @@ int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t*
   }
   GG_HIP(c, hipMemcpy(c->staging, bytes, need, hipMemcpyHostToDevice));
   GG_TRY(launch_rc(c, launch_repack(c->staging, dst, *lay, rows, off, half, c->stream), "repack"));
+  if (layer >= 0 && c->c.prefill_batch > 0) {
+    Layer& Ly = c->layers[layer];
+    uint16_t* wb = nullptr;
+    float* wd = nullptr;
+    long long boff = off;
+    int bhalf = 0;
+    switch (bit) {
+      case Q_ATTN_Q: case Q_ATTN_K: case Q_ATTN_V: wb = Ly.qkv_b; wd = Ly.qkv_d; break;
+      case Q_ATTN_O: wb = Ly.o_b; wd = Ly.o_d; break;
+      case Q_GATE: wb = Ly.gu_b; wd = Ly.gu_d; boff = 0; bhalf = 16; break;
+      case Q_UP: wb = Ly.gu_b; wd = Ly.gu_d; boff = 16; bhalf = 16; break;
+      case Q_DOWN: wb = Ly.down_b; wd = Ly.down_d; break;
+      default: break;
+    }
+    GG_TRY(launch_rc(c, launch_q8_bf16(c->staging, wb, wd, rows, (int)K, boff, bhalf, c->stream), "prefill weights"));
+  }
   GG_TRY(sync(c, "repack"));
   if (layer < 0) c->have_embd = true;
   else c->layers[layer].have |= 1u << bit;
@@ -678,7 +709,7 @@ int gg_finalize(gg_ctx* c) {
     const size_t MH = (size_t)M * c->H * 4;
     GG_TRY(dalloc(c, &c->pf_hidden, MH));
     GG_TRY(dalloc(c, &c->pf_residual, MH));
-    GG_TRY(dalloc(c, &c->pf_xn, MH));
+    GG_TRY(dalloc(c, &c->pf_xn, MH));   // bf16 hi + lo planes: 4 bytes per element
     GG_TRY(dalloc(c, &c->pf_o, MH));
     GG_TRY(dalloc(c, &c->pf_qkv, (size_t)M * c->NQKV * 4));
     GG_TRY(dalloc(c, &c->pf_attn, (size_t)M * c->QD * 4));
