@@ -383,6 +383,14 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   const int wi0 = i0 + (wv * ni) / W, wi1 = i0 + ((wv + 1) * ni) / W;
   const int n = (K - tid + NT - 1) / NT;   // x elements this thread owns
 
+  auto issue_weights = [&](Pair* w) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NIF; ++k) {
+      const int it = max(min(wi0 + k, wi1 - 1), i0);
+      load_planes(a.W + (size_t)it * kColBytes, lane, w[k]);
+    }
+  };
+  Pair st[NIF];
   // 1. prologue loads (clamped indices: always issued)
   float v[EPT], res[EPT], wq[EPT], wp[EPT];
   // PRO_ATTN_MERGE: thread t merges x[4t .. 4t+3] (head t / 64) from the
@@ -392,6 +400,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   float4 am_o[kMB];
   int nch = 0, ahd = 0;
   if (PRO == PRO_ATTN_MERGE) {
+    issue_weights(st);
     int t_lo, ch;
     dec_span(a.st->pos, a.attn_window, &t_lo, &ch, &nch);
     ahd = min(tid >> 6, K / kHeadDim - 1);
@@ -424,13 +433,9 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       }
     }
   }
-  // 2. this wave's weight items (clamped into the block's range)
-  Pair st[NIF];
-#pragma unroll
-  for (int k = 0; k < NIF; ++k) {
-    const int it = max(min(wi0 + k, wi1 - 1), i0);
-    load_planes(a.W + (size_t)it * kColBytes, lane, st[k]);
-  }
+  // 2. this wave's weight items (clamped into the block's range); with
+  // ATTN_MERGE they went out first, ahead of the position-dependent chunk loads
+  if (PRO != PRO_ATTN_MERGE) issue_weights(st);
   for (int i = tid; i < W * kMgRows; i += NT) (&red[0][0])[i] = 0.f;
 
   // 3. prologue -> x in LDS
@@ -578,36 +583,47 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention (one KV head, head_dim 256, up to 4 query heads), one
-// chunk of positions per block; the chunk partials (max, sum, o) go to
-// memory and the attention output projection merges them in its prologue
-// (no cross-block step here). Chunks: 32 * ceil(span / (32 * mc)) positions,
-// mc = 16 while the span is <= 4096 (else kDecMaxChunks), so the merge reads
-// at most 16 partials per head at Gemma-3 1B lengths.
+// Decode attention (one KV head, head_dim 256, up to 4 query heads). Block
+// (x, y) = (chunk of positions, query head); the chunk partials (max, sum, o)
+// go to memory and the attention output projection merges them in its
+// prologue (no cross-block step here). Chunks: 32 * ceil(span / (32 * mc))
+// positions, mc = 16 while the span is <= 4096 (else kDecMaxChunks), so the
+// merge reads at most 16 partials per head at Gemma-3 1B lengths. One head
+// per block keeps each wave's serial chain short (the pass is bound by
+// instruction latency, not by the K/V bytes).
 //
-// Per block: QK-norm + NEOX RoPE of the query heads (wave h: head h) and, in
-// the block holding `pos`, of the key; that block also stores k/v to the
-// cache (fusedPerHeadNormRope + kvCacheStore, shaders.ts:209-227, 420-467).
-// Wave w then runs passes of 8 positions t0 + 32 p + 8 w + i: lane (i, o)
-// = (lane / 8, lane % 8) holds key dims 4 (o + 8 j) .. +3 (j < 8), so each
-// key load instruction reads 8 whole 128-byte segments, and the dot products
-// finish with a butterfly over the 8 lanes of a position; lane l holds value
-// dims 4 l .. 4 l + 3 for the weighted sum (shaders.ts:229-325). Softmax
-// statistics are kept online per pass; all reductions run on DPP (no LDS
-// round trips), probabilities reach every lane through readlane.
+// Per block: QK-norm + NEOX RoPE of query head y and, in the chunk holding
+// `pos`, of the key; that chunk's head-0 block also stores k/v to the cache
+// (fusedPerHeadNormRope + kvCacheStore, shaders.ts:209-227, 420-467). Wave w
+// then runs passes of 8 positions t0 + 32 p + 8 w + i: lane (i, o) =
+// (lane / 8, lane % 8) holds key dims 4 (o + 8 j) .. +3 (j < 8), so each key
+// load instruction reads 8 whole 128-byte segments, and the dot product
+// finishes with a butterfly over the 8 lanes of a position; lane l holds
+// value dims 4 l .. 4 l + 3 for the weighted sum (shaders.ts:229-325).
+// Softmax statistics are kept online per pass; all reductions run on DPP,
+// probabilities reach every lane through readlane.
 // ---------------------------------------------------------------------------
-
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
-  constexpr int NQ = kAttnMaxQ;
-  __shared__ float4 qs4[NQ][64];
+  __shared__ float4 qs4[64];
   __shared__ float4 ks4[64], vs4[64];
-  __shared__ float4 wo[4][NQ][64];
-  __shared__ float wm[4][NQ], wl[4][NQ], fw[4][NQ];
-  __shared__ float hst[NQ][2];
+  __shared__ float4 wo[4][64];
+  __shared__ float wm[4], wl[4], fw[4], hst[2];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
   const int nqd = nq * kHeadDim;
+  const int h = blockIdx.y;
+  // loads that do not depend on the position: q of head h, this token's k
+  // and v, the norm weights
+  float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hx[i] = a.qkv[h * kHeadDim + lane + 64 * i];
+    nwt[i] = a.q_norm[lane + 64 * i];
+    kx[i] = a.qkv[nqd + lane + 64 * i];
+    kwt[i] = a.k_norm[lane + 64 * i];
+  }
+  const float4 vme = *(const float4*)(a.qkv + nqd + kHeadDim + 4 * lane);
   const int pos = a.st->pos;
   int t_lo, ch, nch;
   dec_span(pos, a.window, &t_lo, &ch, &nch);
@@ -637,25 +653,16 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
       vr[i] = *(const float4*)(a.v_cache + (size_t)t * kHeadDim + 4 * lane);
     }
   };
-  load_k(0);
-  load_v(0);
-  // the QKV output, norm weights and this position's RoPE row
-  const bool my_head = wv < nq;
-  float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hx[i] = a.qkv[min(wv, nq - 1) * kHeadDim + lane + 64 * i];
-    nwt[i] = a.q_norm[lane + 64 * i];
-    kx[i] = a.qkv[nqd + lane + 64 * i];
-    kwt[i] = a.k_norm[lane + 64 * i];
-  }
+  // this position's RoPE row, then the first pass of K / V rows (the norm
+  // below waits only for the loads issued before these)
   const float* rt = a.rope + (size_t)pos * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     cs[j] = rt[lane + 64 * j];
     sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
   }
-  const float4 vme = *(const float4*)(a.qkv + nqd + kHeadDim + 4 * lane);
+  load_k(0);
+  load_v(0);
 
   // RMSNorm + NEOX RoPE of one head: lane owns dims lane + 64 i; pairs (i, i + 128)
   auto norm_rope = [&](float* x, const float* w, float* dst) {
@@ -673,32 +680,22 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
       dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
     }
   };
-  if (my_head) norm_rope(hx, nwt, (float*)qs4[wv]);
-  else if (wv < NQ) qs4[wv][lane] = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (holder && wv == 0) norm_rope(kx, kwt, (float*)ks4);
-  if (holder && wv == 1) vs4[lane] = vme;
+  if (wv == 0) norm_rope(hx, nwt, (float*)qs4);
+  if (holder && wv == 1) norm_rope(kx, kwt, (float*)ks4);
+  if (holder && wv == 2) vs4[lane] = vme;
   __syncthreads();
-  if (holder) {
+  if (holder && h == 0) {
     a.k_cache[(size_t)pos * kHeadDim + tid] = ((const float*)ks4)[tid];
     a.v_cache[(size_t)pos * kHeadDim + tid] = ((const float*)vs4)[tid];
   }
-  if (b == 0 && a.q_dbg)
-    for (int e = tid; e < nqd; e += 256) a.q_dbg[e] = ((const float*)qs4[e >> 8])[e & 255];
+  if (b == 0 && a.q_dbg && tid < 64) *(float4*)(a.q_dbg + h * kHeadDim + 4 * tid) = qs4[tid];
 
-  float4 qr[NQ][8];
+  float4 qr[8];
 #pragma unroll
-  for (int h = 0; h < NQ; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qr[h][j] = qs4[h][oc + 8 * j];
+  for (int j = 0; j < 8; ++j) qr[j] = qs4[oc + 8 * j];
 
-  float m[NQ], l[NQ];
-  float4 o4[NQ];
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
-    o4[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  float m = -INFINITY, l = 0.f;
+  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int p = 0; p < npass; ++p) {
     const int tb = t0 + 32 * p + 8 * wv;       // first position of this wave's pass
     const int t = tb + pl;
@@ -706,90 +703,76 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = ks4[oc + 8 * j];
     }
-    float sc[NQ];
+    float d = 0.f;
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      float d = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        d = fmaf(qr[h][j].x, kr[j].x, d);
-        d = fmaf(qr[h][j].y, kr[j].y, d);
-        d = fmaf(qr[h][j].z, kr[j].z, d);
-        d = fmaf(qr[h][j].w, kr[j].w, d);
-      }
-      d = group8_sum(d);
-      sc[h] = (t < t1 && h < nq) ? d * a.scale : -INFINITY;
+    for (int j = 0; j < 8; ++j) {
+      d = fmaf(qr[j].x, kr[j].x, d);
+      d = fmaf(qr[j].y, kr[j].y, d);
+      d = fmaf(qr[j].z, kr[j].z, d);
+      d = fmaf(qr[j].w, kr[j].w, d);
     }
+    d = group8_sum(d);
+    const float sc = (t < t1) ? d * a.scale : -INFINITY;
     load_k(p + 1 < npass ? p + 1 : p);          // next pass (a repeat on the last)
-    float pr[NQ], alpha[NQ];
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      const float mx = across8_max(sc[h]);
-      const float mn = fmaxf(m[h], mx);
-      alpha[h] = (m[h] == -INFINITY) ? 0.f : expf(m[h] - mn);
-      pr[h] = (sc[h] == -INFINITY) ? 0.f : expf(sc[h] - mn);
-      l[h] = fmaf(l[h], alpha[h], across8_sum(pr[h]));
-      m[h] = mn;
-    }
+    const float mx = across8_max(sc);
+    const float mn = fmaxf(m, mx);
+    const float alpha = (m == -INFINITY) ? 0.f : expf(m - mn);
+    const float pr = (sc == -INFINITY) ? 0.f : expf(sc - mn);
+    l = fmaf(l, alpha, across8_sum(pr));
+    m = mn;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (tb + i == pos) vr[i] = vs4[lane];
+    o4.x *= alpha;
+    o4.y *= alpha;
+    o4.z *= alpha;
+    o4.w *= alpha;
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) {
-      o4[h].x *= alpha[h];
-      o4[h].y *= alpha[h];
-      o4[h].z *= alpha[h];
-      o4[h].w *= alpha[h];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[h]), 8 * i));
-        o4[h].x = fmaf(pv, vr[i].x, o4[h].x);
-        o4[h].y = fmaf(pv, vr[i].y, o4[h].y);
-        o4[h].z = fmaf(pv, vr[i].z, o4[h].z);
-        o4[h].w = fmaf(pv, vr[i].w, o4[h].w);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), 8 * i));
+      o4.x = fmaf(pv, vr[i].x, o4.x);
+      o4.y = fmaf(pv, vr[i].y, o4.y);
+      o4.z = fmaf(pv, vr[i].z, o4.z);
+      o4.w = fmaf(pv, vr[i].w, o4.w);
     }
     load_v(p + 1 < npass ? p + 1 : p);
   }
 
   // merge the four waves (fixed order) into the chunk's (max, sum, o)
-#pragma unroll
-  for (int h = 0; h < NQ; ++h) wo[wv][h][lane] = o4[h];
+  wo[wv][lane] = o4;
   if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) { wm[wv][h] = m[h]; wl[wv][h] = l[h]; }
+    wm[wv] = m;
+    wl[wv] = l;
   }
   __syncthreads();
-  if (tid < NQ) {
-    const int h = tid;
-    const float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+  if (tid == 0) {
+    const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = wm[w][h] == -INFINITY ? 0.f : expf(wm[w][h] - M);
-      fw[w][h] = f;
-      L = fmaf(f, wl[w][h], L);
+      const float f = wm[w] == -INFINITY ? 0.f : expf(wm[w] - M);
+      fw[w] = f;
+      L = fmaf(f, wl[w], L);
     }
-    hst[h][0] = M;
-    hst[h][1] = L;
+    hst[0] = M;
+    hst[1] = L;
   }
   __syncthreads();
-  const int h = tid >> 6, q = tid & 63;       // thread: head h, dims 4 q .. 4 q + 3
-  if (h < nq) {
+  if (tid < 64) {
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = fw[w][h];
-      const float4 v = wo[w][h][q];
+      const float f = fw[w];
+      const float4 v = wo[w][tid];
       O.x = fmaf(f, v.x, O.x);
       O.y = fmaf(f, v.y, O.y);
       O.z = fmaf(f, v.z, O.z);
       O.w = fmaf(f, v.w, O.w);
     }
-    *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * q) = O;
-    if (q == 0) {
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[h][0];
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[h][1];
+    *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = O;
+    if (tid == 0) {
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[0];
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[1];
     }
   }
 }
@@ -1609,7 +1592,7 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
   if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kDecMaxChunks) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_dec, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_attn_dec, dim3(grid, a.n_q), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
