@@ -104,7 +104,7 @@ struct GemvArgs {
   // PRO_ATTN_MERGE (attention output projection): x is the merge of the
   // decode attention chunk partials of this token
   const float* attn_part;  // o [kDecMaxChunks][kAttnMaxQ][256], then (m, l) [kDecMaxChunks][kAttnMaxQ][2]
-  int attn_window;         // the layer's sliding window (0: full causal)
+  int attn_chunks;         // chunks the attention launch wrote (blocks past the span leave empty ones)
   float* x_out;            // block 0 stores the merged x here (the attention output)
 };
 
@@ -203,8 +203,11 @@ enum Epilogue { EPI_OUT = 0, EPI_GEGLU = 1 };
 
 int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream);
 int launch_attention(const AttnArgs& a, int grid, void* stream);
-// decode attention grid for a context length: 16 chunks up to span 4096, else kDecMaxChunks
-inline int decode_attention_grid(int ctx) { return ctx <= 4096 ? 16 : kDecMaxChunks; }
+// Decode attention chunks of a layer: 16 while its span cannot exceed 4096
+// positions (a window <= 4096, or a context <= 4096), else kDecMaxChunks.
+inline int decode_attention_chunks(int ctx, int window) {
+  return (ctx <= 4096 || (window > 0 && window <= 4096)) ? 16 : kDecMaxChunks;
+}
 int launch_final(const FinalArgs& a, void* stream);
 int launch_select(const SelectArgs& a, void* stream);
 int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,

@@ -401,8 +401,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   int nch = 0, ahd = 0;
   if (PRO == PRO_ATTN_MERGE) {
     issue_weights(st);
-    int t_lo, ch;
-    dec_span(a.st->pos, a.attn_window, &t_lo, &ch, &nch);
+    nch = a.attn_chunks;   // every chunk of the launch, empty ones included: no wait for the position
     ahd = min(tid >> 6, K / kHeadDim - 1);
 #pragma unroll
     for (int k = 0; k < kMB; ++k) {
@@ -588,7 +587,9 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 // go to memory and the attention output projection merges them in its
 // prologue (no cross-block step here). Chunks: 32 * ceil(span / (32 * mc))
 // positions, mc = 16 while the span is <= 4096 (else kDecMaxChunks), so the
-// merge reads at most 16 partials per head at Gemma-3 1B lengths. One head
+// merge reads at most 16 partials per head at Gemma-3 1B lengths. Blocks past
+// the span write empty partials (m = -inf), so the merge always reads the
+// launch's chunk count and does not wait for the position. One head
 // per block keeps each wave's serial chain short (the pass is bound by
 // instruction latency, not by the K/V bytes).
 //
@@ -628,7 +629,14 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
   int t_lo, ch, nch;
   dec_span(pos, a.window, &t_lo, &ch, &nch);
   const int b = blockIdx.x;
-  if (b >= nch) return;
+  if (b >= nch) {   // past the span: an empty partial, so that the merge needs no position
+    if (tid < 64) *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid == 0) {
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = -INFINITY;
+      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = 0.f;
+    }
+    return;
+  }
   const int t0 = t_lo + b * ch;
   const int t1 = min(t0 + ch, pos + 1);
   const int npass = (t1 - t0 + 31) >> 5;
@@ -1578,7 +1586,8 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
   if (epi == EPI_GEGLU && pro != PRO_RESID_NORM) return (int)hipErrorInvalidValue;
   MgPlan plan;
   if (pro == PRO_ATTN_MERGE) {   // only the multi-group kernel merges: K = n_q * 256 <= 1024 on 256 threads
-    if (ci == 1 || a.Kp * 64 > kAttnMaxQ * kHeadDim || a.Kp % 4 || !mg_plan(a, pro, ci, plan))
+    if (ci == 1 || a.Kp * 64 > kAttnMaxQ * kHeadDim || a.Kp % 4 || a.attn_chunks < 1 ||
+        a.attn_chunks > kDecMaxChunks || !mg_plan(a, pro, ci, plan))
       return (int)hipErrorInvalidValue;
     return launch_mg(pro, epi, ci, a, plan, s);
   }

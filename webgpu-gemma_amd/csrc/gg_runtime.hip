@@ -101,7 +101,6 @@ struct gg_ctx {
   int32_t* d_ids = nullptr;           // staging for gg_penalty_add
   uint8_t* staging = nullptr;         // Q8_0 upload staging
   size_t staging_bytes = 0;
-  int attn_grid = 1;
 
   // batched prefill (prefill_batch > 0)
   int pf_M = 0;
@@ -254,12 +253,12 @@ int record_forward(gg_ctx* c) {
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
     {
       ProbeScope ps(c, GG_PROBE_ATTN, l);
-      GG_TRY(launch_rc(c, launch_attention(at, c->attn_grid, c->stream), "attention"));
+      GG_TRY(launch_rc(c, launch_attention(at, decode_attention_chunks(c->CTX, at.window), c->stream), "attention"));
     }
     // O projection; its prologue merges the attention chunks into attn_out
     GemvArgs o = gemv_base(Ly.o, c->lay_o, c->o_out);
     o.attn_part = c->attn_part;
-    o.attn_window = at.window;
+    o.attn_chunks = decode_attention_chunks(c->CTX, at.window);
     o.x_out = c->attn_out;
     o.st = c->st;
     {
@@ -671,7 +670,6 @@ int gg_finalize(gg_ctx* c) {
       return set_err(c, GG_ERR_MISSING, "missing tensors of blk." + std::to_string(l));
   if (c->staging) { (void)hipFree(c->staging); c->staging = nullptr; c->staging_bytes = 0; }
 
-  c->attn_grid = decode_attention_grid(c->CTX);
 
   const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
   for (Layer& Ly : c->layers) {
