@@ -1,4 +1,4 @@
-"""Batched prefill (M-row GEMMs on fp32 MFMA + batched attention) against the
+"""Batched prefill (M-row GEMMs on bf16 MFMA + MFMA flash attention) against the
 oracle's token-by-token prefill (engine.ts:923-928) and against the GPU's own
 per-token path at the Gemma-3-1B shape."""
 import numpy as np
