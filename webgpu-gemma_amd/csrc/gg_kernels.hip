@@ -381,7 +381,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   const int g0 = (int)(((long long)b * G) / nb), g1 = (int)(((long long)(b + 1) * G) / nb);
   const int i0 = g0 * KpS, ni = (g1 - g0) * KpS;
   const int wi0 = i0 + (wv * ni) / W, wi1 = i0 + ((wv + 1) * ni) / W;
-  const int n = (K - tid + NT - 1) / NT;   // x elements this thread owns
+  const int K4 = K / 4;   // thread t owns the float4 chunks t + NT i (i < EPT) of x
 
   auto issue_weights = [&](Pair* w) __attribute__((always_inline)) {
 #pragma unroll
@@ -391,8 +391,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     }
   };
   Pair st[NIF];
-  // 1. prologue loads (clamped indices: always issued)
-  float v[EPT], res[EPT], wq[EPT], wp[EPT];
+  // 1. prologue loads (16 bytes per lane, clamped indices: always issued)
+  float4 v[EPT], res[EPT], wq[EPT], wp[EPT];
   // PRO_ATTN_MERGE: thread t merges x[4t .. 4t+3] (head t / 64) from the
   // first 16 chunk partials (more are merged in batches of 16 below)
   constexpr int kMB = 16;
@@ -402,33 +402,36 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   if (PRO == PRO_ATTN_MERGE) {
     issue_weights(st);
     nch = a.attn_chunks;   // every chunk of the launch, empty ones included: no wait for the position
-    ahd = min(tid >> 6, K / kHeadDim - 1);
+    // head of this wave (uniform): its (max, sum) pairs come through scalar loads
+    ahd = __builtin_amdgcn_readfirstlane(min(wv, K / kHeadDim - 1));
 #pragma unroll
     for (int k = 0; k < kMB; ++k) {
       const int c = min(k, nch - 1);
-      am_m[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2];
-      am_l[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2 + 1];
+      const float2 ml = *(const float2*)(a.attn_part + kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2);
+      am_m[k] = ml.x;
+      am_l[k] = ml.y;
       am_o[k] = *(const float4*)(a.attn_part + ((size_t)c * kAttnMaxQ + ahd) * kHeadDim + 4 * (tid & 63));
     }
   } else if (PRO == PRO_EMBED_NORM) {
     const int token = a.tokens[a.st->cursor];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int e = min(tid + NT * i, K - 1);
-      v[i] = embed_elem(a, token, e);
-      wp[i] = a.w_pre[e];
+      const int c = min(tid + NT * i, K4 - 1);
+      v[i] = make_float4(embed_elem(a, token, 4 * c), embed_elem(a, token, 4 * c + 1),
+                         embed_elem(a, token, 4 * c + 2), embed_elem(a, token, 4 * c + 3));
+      wp[i] = ((const float4*)a.w_pre)[c];
     }
   } else {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int e = min(tid + NT * i, K - 1);
+      const int c = min(tid + NT * i, K4 - 1);
       if (PRO == PRO_NONE) {
-        v[i] = a.x[e];
+        v[i] = ((const float4*)a.x)[c];
       } else {
-        v[i] = a.pre_vec[e];
-        res[i] = a.pre_res[e];
-        wq[i] = a.w_post[e];
-        wp[i] = a.w_pre[e];
+        v[i] = ((const float4*)a.pre_vec)[c];
+        res[i] = ((const float4*)a.pre_res)[c];
+        wq[i] = ((const float4*)a.w_post)[c];
+        wp[i] = ((const float4*)a.w_pre)[c];
       }
     }
   }
@@ -438,10 +441,17 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   for (int i = tid; i < W * kMgRows; i += NT) (&red[0][0])[i] = 0.f;
 
   // 3. prologue -> x in LDS
+  auto has = [&](int i) { return tid + NT * i < K4; };
+  auto sq4 = [](float4 q, float acc) {
+    acc = fmaf(q.x, q.x, acc);
+    acc = fmaf(q.y, q.y, acc);
+    acc = fmaf(q.z, q.z, acc);
+    return fmaf(q.w, q.w, acc);
+  };
   if (PRO == PRO_NONE) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-      if (i < n) xs[xs_index(tid + NT * i)] = v[i];
+      if (has(i)) *(float4*)&xs[xs_index(4 * (tid + NT * i))] = v[i];
   } else if (PRO == PRO_ATTN_MERGE) {
     // chunk weights exp(m_c - M) with M the running max, in chunk order
     float M = -INFINITY;
@@ -465,8 +475,9 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 #pragma unroll
       for (int k = 0; k < kMB; ++k) {
         const int c = min(c0 + k, nch - 1);
-        am_m[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2];
-        am_l[k] = a.attn_part[kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2 + 1];
+        const float2 ml = *(const float2*)(a.attn_part + kDecStatOff + ((size_t)c * kAttnMaxQ + ahd) * 2);
+        am_m[k] = ml.x;
+        am_l[k] = ml.y;
         am_o[k] = *(const float4*)(a.attn_part + ((size_t)c * kAttnMaxQ + ahd) * kHeadDim + 4 * (tid & 63));
       }
       float Mb = M;
@@ -490,7 +501,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       if (b == 0) *(float4*)(a.x_out + 4 * tid) = xo;
     }
   } else {
-    float r[EPT];
+    float4 r[EPT];
     if (PRO == PRO_EMBED_NORM) {
 #pragma unroll
       for (int i = 0; i < EPT; ++i) r[i] = v[i];
@@ -498,7 +509,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       float s1 = 0.f;
 #pragma unroll
       for (int i = 0; i < EPT; ++i)
-        if (i < n) s1 = fmaf(v[i], v[i], s1);
+        if (has(i)) s1 = sq4(v[i], s1);
       s1 = wave_sum_dpp(s1);
       if (lane == 0) shw[0][wv] = s1;
       __syncthreads();
@@ -507,18 +518,20 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       for (int w = 0; w < W; ++w) t1 += shw[0][w];
       const float rms1 = sqrtf(t1 / (float)K + a.eps);
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) r[i] = res[i] + (v[i] * wq[i]) / rms1;
+      for (int i = 0; i < EPT; ++i)
+        r[i] = make_float4(res[i].x + (v[i].x * wq[i].x) / rms1, res[i].y + (v[i].y * wq[i].y) / rms1,
+                           res[i].z + (v[i].z * wq[i].z) / rms1, res[i].w + (v[i].w * wq[i].w) / rms1);
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-      if (i < n) ss = fmaf(r[i], r[i], ss);
+      if (has(i)) ss = sq4(r[i], ss);
     if (b == 0) {
 #pragma unroll
       for (int i = 0; i < EPT; ++i)
-        if (i < n) {
-          a.res_out[tid + NT * i] = r[i];
-          if (PRO == PRO_RESID_NORM && a.hist_out) a.hist_out[tid + NT * i] = r[i];
+        if (has(i)) {
+          ((float4*)a.res_out)[tid + NT * i] = r[i];
+          if (PRO == PRO_RESID_NORM && a.hist_out) ((float4*)a.hist_out)[tid + NT * i] = r[i];
         }
     }
     ss = wave_sum_dpp(ss);
@@ -530,7 +543,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     const float rms = sqrtf(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-      if (i < n) xs[xs_index(tid + NT * i)] = (r[i] * wp[i]) / rms;
+      if (has(i))
+        *(float4*)&xs[xs_index(4 * (tid + NT * i))] =
+            make_float4((r[i].x * wp[i].x) / rms, (r[i].y * wp[i].y) / rms, (r[i].z * wp[i].z) / rms,
+                        (r[i].w * wp[i].w) / rms);
   }
   __syncthreads();
 
@@ -1525,8 +1541,8 @@ static bool mg_plan(const GemvArgs& a, int pro, int ci, MgPlan& p) {
   const int K = a.Kp * 64, GR = 64 / ci, G = a.N / GR;
   p.W = K > 2048 ? 16 : 4;
   if ((pro != PRO_NONE || ci != 8) && p.W != 4) return false;
-  const int ept = (K + 64 * p.W - 1) / (64 * p.W);
-  p.ept = ept <= 2 ? ept : ept <= 4 ? 4 : ept <= 5 ? 5 : 8;
+  p.ept = (K / 4 + 64 * p.W - 1) / (64 * p.W);   // float4 chunks of x per thread: 1 or 2
+  if (p.ept > 2) return false;
   int nb = min(G, p.W == 4 ? 512 : 256);
   for (;;) {
     const int gpb = (G + nb - 1) / nb;
@@ -1547,7 +1563,7 @@ static int launch_mg_ept(const GemvArgs& a, const MgPlan& p, hipStream_t s) {
   switch (p.ept) {
 #define GG_MG_EPT(E) \
     case E: hipLaunchKernelGGL((k_gemv_mg<PRO, EPI, CI, W, NIF, E>), dim3(p.nb), dim3(64 * W), lds, s, a); break;
-    GG_MG_EPT(1) GG_MG_EPT(2) GG_MG_EPT(4) GG_MG_EPT(5) GG_MG_EPT(8)
+    GG_MG_EPT(1) GG_MG_EPT(2)
 #undef GG_MG_EPT
     default: return (int)hipErrorInvalidValue;
   }
