@@ -71,11 +71,12 @@ inline Q8Layout q8_layout(int rows, int K, int force_ci = 0) {
 // `seen_count` and `out_token` are maintained by the kernels.
 struct DevState {
   int32_t pos;          // position of the token being processed
-  int32_t cursor;       // index into the device token array
+  int32_t cursor;       // index into the device token array; < 0: embed `token`
   double temperature;
   double top_p;
   double rep_penalty;
   double u;             // uniform draw in [0,1) injected by the host
+  int32_t token;        // gg_step: the token to embed (cursor < 0)
   int32_t seen_count;   // number of ids added to the penalty bitmap
   int32_t out_token;    // last selected token
 };
@@ -195,6 +196,7 @@ struct SelectArgs {
   uint32_t* seen;          // [ceil(V/32)] penalty bitmap
   DevState* st;
   int auto_add;            // add the chosen id to the bitmap
+  int32_t* host_out;       // optional: mapped pinned host word that also receives the token
 };
 
 // ---- launchers (gg_kernels.hip) -------------------------------------------

@@ -223,7 +223,8 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
   float r[kMaxEPT / 4], wp[kMaxEPT / 4];  // K <= 2048 for the norm prologues
   float ss = 0.f;
   if (PRO == PRO_EMBED_NORM) {
-    const int token = a.tokens[a.st->cursor];
+    const int cur = a.st->cursor;
+    const int token = cur < 0 ? a.st->token : a.tokens[cur];
 #pragma unroll
     for (int i = 0; i < kMaxEPT / 4; ++i)
       if (i < n) {
@@ -413,7 +414,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       am_o[k] = *(const float4*)(a.attn_part + ((size_t)c * kAttnMaxQ + ahd) * kHeadDim + 4 * (tid & 63));
     }
   } else if (PRO == PRO_EMBED_NORM) {
-    const int token = a.tokens[a.st->cursor];
+    const int cur = a.st->cursor;
+    const int token = cur < 0 ? a.st->token : a.tokens[cur];
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int c = min(tid + NT * i, K4 - 1);
@@ -980,6 +982,7 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
   }
   if (tid == 0) {
     a.st->out_token = token;
+    if (a.host_out) a.host_out[0] = token;
     if (a.auto_add && token >= 0 && token < a.V) {
       a.seen[token >> 5] |= 1u << (token & 31);
       a.st->seen_count += 1;

@@ -111,7 +111,8 @@ struct gg_ctx {
   // pinned host mirrors
   DevState* h_st = nullptr;
   int32_t* h_tokens = nullptr;
-  int32_t* h_out = nullptr;
+  int32_t* h_out = nullptr;           // mapped: the selector writes the token here
+  int32_t* d_out = nullptr;           // h_out's device address
 
   hipGraphExec_t g_fwd = nullptr, g_sel = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -317,6 +318,7 @@ int record_select(gg_ctx* c) {
   s.seen = c->seen;
   s.st = c->st;
   s.auto_add = 1;
+  s.host_out = c->d_out;
   ProbeScope ps(c, GG_PROBE_SELECT, -1);
   return launch_rc(c, launch_select(s, c->stream), "select");
 }
@@ -746,9 +748,11 @@ int gg_finalize(gg_ctx* c) {
 
   GG_HIP(c, hipHostMalloc((void**)&c->h_st, sizeof(DevState), hipHostMallocDefault));
   GG_HIP(c, hipHostMalloc((void**)&c->h_tokens, (size_t)c->CTX * 4, hipHostMallocDefault));
-  GG_HIP(c, hipHostMalloc((void**)&c->h_out, 64, hipHostMallocDefault));
+  GG_HIP(c, hipHostMalloc((void**)&c->h_out, 64, hipHostMallocMapped | hipHostMallocCoherent));
+  GG_HIP(c, hipHostGetDevicePointer((void**)&c->d_out, c->h_out, 0));
   memset(c->h_st, 0, sizeof(DevState));
-  for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreate(&c->ev[i]));
+  // timing events only: no system-scope fence (an L2 write-back) per record
+  for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->ev[i], hipEventDisableSystemFence));
   if (c->probe_kind != GG_PROBE_NONE)
     // timing-only events: no system-scope fence (cache write-back/invalidate)
     // around the bracketed launch
@@ -806,8 +810,7 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
   GG_TRY(run_select(c));
   GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
-  GG_HIP(c, hipMemcpyAsync(c->h_out, (char*)c->st + offsetof(DevState, out_token), 4, hipMemcpyDeviceToHost,
-                           c->stream));
+  // the selector stores the token straight into the mapped host word
   GG_TRY(sync(c, with_forward ? "step" : "select"));
   c->timed = true;
   *out = c->h_out[0];
@@ -825,10 +828,9 @@ int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u,
   if (!s || !out_token) return set_err(c, GG_ERR_INVALID, "null argument");
   if (token < 0 || token >= c->V) return set_err(c, GG_ERR_INVALID, "token id out of range");
   if (pos < 0 || pos >= c->CTX) return set_err(c, GG_ERR_INVALID, "position outside the context");
-  c->h_tokens[0] = token;
   c->h_st->pos = pos;
-  c->h_st->cursor = 0;
-  GG_HIP(c, hipMemcpyAsync(c->tokens, c->h_tokens, 4, hipMemcpyHostToDevice, c->stream));
+  c->h_st->cursor = -1;   // embed DevState.token: one state upload per step
+  c->h_st->token = token;
   return select_impl(c, s, u, out_token, true);
 }
 
