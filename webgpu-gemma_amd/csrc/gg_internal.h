@@ -143,7 +143,8 @@ struct GemmArgs {
   const uint16_t* W;       // [N][K]
   const float* D;          // [N][K / 32]
   int M, N, K;
-  float* C;                // EPI_OUT: [M][N]
+  int ks;                  // K slices (1..kGemmMaxSlices, EPI_OUT only): slice z covers K/ks and writes C + z M N
+  float* C;                // EPI_OUT: [M][N] per slice
   uint16_t* act;           // EPI_GEGLU: hi plane [M][N/2], then lo plane; gate / up rows
                            // alternate in groups of 16 (16 gate rows, then their up rows)
 };
@@ -158,6 +159,8 @@ struct RowArgs {
   int embd_KpS;
   float embed_scale;
   const float* pre;        // RESID: output of the previous GEMM [M][H]
+  int pre_planes;          // K slices of `pre` to add (0 or 1: one)
+  size_t pre_stride;       // floats between the slices
   const float* res;        // RESID: residual stream entering the add [M][H]
   const float* w_post;
   const float* w_pre;
@@ -176,6 +179,8 @@ struct RowArgs {
 
 struct FinalArgs {
   const float* pre_vec;
+  int pre_planes;          // K slices of pre_vec to add (0 or 1: one)
+  size_t pre_stride;       // floats between the slices
   const float* pre_res;
   const float* w_post;
   const float* w_out;
@@ -225,6 +230,7 @@ int launch_gemm(int epi, const GemmArgs& a, void* stream);
 int launch_rows_embed(const RowArgs& a, void* stream);
 int launch_rows_resid(const RowArgs& a, void* stream);
 int launch_rows_kv(const RowArgs& a, void* stream);
+constexpr int kGemmMaxSlices = 4;   // K slices of a prefill GEMM (summed by the consumer)
 constexpr int kPrefillChunks = 16;   // key chunks per query tile in the batched prefill attention
 constexpr int kPrefillMinChunk = 256;
 // Longest key span of a 16-row query tile of a prefill of M rows at `start`.

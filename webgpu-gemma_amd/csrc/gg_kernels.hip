@@ -817,6 +817,7 @@ __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
     if (i < n) {
       const int e = tid + 256 * i;
       v[i] = a.pre_vec[e];
+      for (int p = 1; p < a.pre_planes; ++p) v[i] += a.pre_vec[p * a.pre_stride + e];
       res[i] = a.pre_res[e];
       wq[i] = a.w_post[e];
       wo[i] = a.w_out[e];
@@ -1254,6 +1255,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.M, K = a.K;
   const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
+  const int kz = blockIdx.z, kn = K / a.ks;   // this block's K slice [kz kn, (kz + 1) kn)
   const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
   const size_t MK = (size_t)M * K;
   // staging: rows tid / 8 + 32 i, 16-byte chunk tid % 8 of the 64-wide step;
@@ -1290,12 +1292,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  for (int k0 = 0; k0 < K; k0 += 64) {
+  const int kb = kz * kn, ke = kb + kn;
+  fetch(kb);
+  for (int k0 = kb; k0 < ke; k0 += 64) {
     __syncthreads();   // the previous step's LDS reads are done
     stage();
     __syncthreads();
-    if (k0 + 64 < K) fetch(k0 + 64);
+    if (k0 + 64 < ke) fetch(k0 + 64);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       bf16x8 xh[4], xl[4], w[4];
@@ -1334,7 +1337,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + wn + 16 * j + c16;
         if (EPI == EPI_OUT) {
-          a.C[(size_t)m * a.N + n] = acc[i][j][r];
+          a.C[(size_t)kz * M * a.N + (size_t)m * a.N + n] = acc[i][j][r];
         } else if ((j & 1) == 0) {
           // 16 gate rows (tile j), then their 16 up rows (tile j + 1)
           const size_t o = (size_t)m * (a.N / 2) + (n >> 5) * 16 + (n & 15);
@@ -1389,6 +1392,7 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
   for (int i = 0; i < 8; ++i)
     if (i < n) {
       v[i] = a.pre[o + tid + 256 * i];
+      for (int p = 1; p < a.pre_planes; ++p) v[i] += a.pre[p * a.pre_stride + o + tid + 256 * i];
       rs[i] = a.res[o + tid + 256 * i];
       wq[i] = a.w_post[tid + 256 * i];
     }
@@ -1679,10 +1683,10 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
 }
 
 int launch_gemm(int epi, const GemmArgs& a, void* stream) {
-  if (a.M < 1 || a.N < kGBN || a.N % kGBN || a.K < 64 || a.K % 64 || !a.A || !a.W || !a.D ||
-      (epi == EPI_OUT ? !a.C : !a.act))
+  if (a.M < 1 || a.N < kGBN || a.N % kGBN || a.K < 64 || a.ks < 1 || a.ks > kGemmMaxSlices || a.K % (64 * a.ks) ||
+      !a.A || !a.W || !a.D || (epi == EPI_OUT ? !a.C : (!a.act || a.ks != 1)))
     return (int)hipErrorInvalidValue;
-  dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM);
+  dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM, a.ks);
   if (epi == EPI_OUT) hipLaunchKernelGGL(k_gemm<EPI_OUT>, grid, dim3(256), 0, (hipStream_t)stream, a);
   else hipLaunchKernelGGL(k_gemm<EPI_GEGLU>, grid, dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();

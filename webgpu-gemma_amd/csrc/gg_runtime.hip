@@ -365,8 +365,25 @@ int sync(gg_ctx* c, const char* what) {
 }
 
 
+// K slices (up to max_ks, dividing K into whole 64-steps) that minimise the
+// modelled time: steps per block times the load of the busiest CU, where n >= 2
+// co-resident blocks take 0.75 n of one block's time (measured on the 1B down
+// GEMM: 144 blocks x 108 steps 165 us, 288 x 54 124 us). C must hold that many
+// slices; the consumer adds them.
+int gemm_slices(int N, int K, int M, int max_ks) {
+  const int tiles = (N / 128) * ((M + 127) / 128), steps = K / 64;
+  auto cost = [&](int ks) {
+    const int per_cu = (tiles * ks + 255) / 256;
+    return (per_cu == 1 ? 1.0 : 0.75 * per_cu) * (steps / ks);
+  };
+  int best = 1;
+  for (int ks = 2; ks <= max_ks; ++ks)
+    if (steps % ks == 0 && cost(ks) < cost(best)) best = ks;
+  return best;
+}
+
 GemmArgs gemm_base(const uint16_t* A, const uint16_t* W, const float* D, int N, int K, int M, float* C,
-                   uint16_t* act) {
+                   uint16_t* act, int max_ks = 1) {
   GemmArgs g{};
   g.A = A;
   g.W = W;
@@ -376,6 +393,7 @@ GemmArgs gemm_base(const uint16_t* A, const uint16_t* W, const float* D, int N, 
   g.K = K;
   g.C = C;
   g.act = act;
+  g.ks = C ? gemm_slices(N, K, M, max_ks) : 1;
   return g;
 }
 
@@ -427,9 +445,12 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     at.pf_rows = M;
     at.pf_chunk = prefill_chunk(at.window, start, M);
     GG_TRY(launch_rc(c, launch_prefill_attention(at, M, s), "prefill attention"));
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_attn, Ly.o_b, Ly.o_d, c->H, c->QD, M, c->pf_o, nullptr), s), "prefill o"));
+    const GemmArgs go = gemm_base(c->pf_attn, Ly.o_b, Ly.o_d, c->H, c->QD, M, c->pf_o, nullptr, 2);
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, go, s), "prefill o"));
     RowArgs r1 = r;
     r1.pre = c->pf_o;
+    r1.pre_planes = go.ks;
+    r1.pre_stride = (size_t)M * c->H;
     r1.res = c->pf_hidden;
     r1.w_post = Ly.norm[N_POST_ATTN];
     r1.w_pre = Ly.norm[N_FFN];
@@ -437,10 +458,13 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     r1.x_out = c->pf_xn;
     GG_TRY(launch_rc(c, launch_rows_resid(r1, s), "prefill post-attn"));
     GG_TRY(launch_rc(c, launch_gemm(EPI_GEGLU, gemm_base(c->pf_xn, Ly.gu_b, Ly.gu_d, 2 * c->I, c->H, M, nullptr, c->pf_act), s), "prefill gate/up"));
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_act, Ly.down_b, Ly.down_d, c->H, c->I, M, c->pf_o, nullptr), s), "prefill down"));
+    const GemmArgs gd = gemm_base(c->pf_act, Ly.down_b, Ly.down_d, c->H, c->I, M, c->pf_o, nullptr, 3);
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gd, s), "prefill down"));
     if (l + 1 < c->L) {
       RowArgs r2 = r;
       r2.pre = c->pf_o;
+      r2.pre_planes = gd.ks;
+      r2.pre_stride = (size_t)M * c->H;
       r2.res = c->pf_residual;
       r2.w_post = Ly.norm[N_POST_FFW];
       r2.w_pre = c->layers[l + 1].norm[N_ATTN];
@@ -451,6 +475,8 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     } else {
       FinalArgs f{};
       f.pre_vec = c->pf_o + (size_t)(M - 1) * c->H;
+      f.pre_planes = gd.ks;
+      f.pre_stride = (size_t)M * c->H;
       f.pre_res = c->pf_residual + (size_t)(M - 1) * c->H;
       f.w_post = Ly.norm[N_POST_FFW];
       f.w_out = c->out_norm;
@@ -710,7 +736,7 @@ int gg_finalize(gg_ctx* c) {
     GG_TRY(dalloc(c, &c->pf_hidden, MH));
     GG_TRY(dalloc(c, &c->pf_residual, MH));
     GG_TRY(dalloc(c, &c->pf_xn, MH));   // bf16 hi + lo planes: 4 bytes per element
-    GG_TRY(dalloc(c, &c->pf_o, MH));
+    GG_TRY(dalloc(c, &c->pf_o, kGemmMaxSlices * MH));   // K slices of the O / down GEMMs
     GG_TRY(dalloc(c, &c->pf_qkv, (size_t)M * c->NQKV * 4));
     GG_TRY(dalloc(c, &c->pf_attn, (size_t)M * c->QD * 4));
     GG_TRY(dalloc(c, &c->pf_act, (size_t)M * c->I * 4));
