@@ -1254,8 +1254,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.M, K = a.K;
-  const int m0 = blockIdx.y * kGBM, n0 = blockIdx.x * kGBN;
-  const int kz = blockIdx.z, kn = K / a.ks;   // this block's K slice [kz kn, (kz + 1) kn)
+  // Tile order: block b (launch order) runs on XCD b % 8, and XCD x takes the
+  // contiguous range [x G / 8, (x + 1) G / 8) of an order with the K slice
+  // slowest, then groups of 4 tile rows with the rows fastest, so that the
+  // blocks sharing an XCD's L2 share A rows and W tiles (fewer L2 misses).
+  const int NT = gridDim.x, MT = gridDim.y, G = NT * MT * gridDim.z;
+  const int bid = blockIdx.x + NT * (blockIdx.y + MT * blockIdx.z);
+  const int L = (G % 8 == 0) ? (bid % 8) * (G / 8) + bid / 8 : bid;
+  const int kz = L / (NT * MT), Lp = L % (NT * MT);
+  const int fm = (Lp / (4 * NT)) * 4, gm = min(MT - fm, 4);
+  const int m0 = (fm + (Lp % (4 * NT)) % gm) * kGBM, n0 = ((Lp % (4 * NT)) / gm) * kGBN;
+  const int kn = K / a.ks;   // this block's K slice [kz kn, (kz + 1) kn)
   const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
   const size_t MK = (size_t)M * K;
   // staging: rows tid / 8 + 32 i, 16-byte chunk tid % 8 of the 64-wide step;
