@@ -84,9 +84,10 @@ def prefill_flops(shape, m: int):
 
 def prefill_report(shape, args, prefill_s: float) -> dict:
     """TTFT and MFMA utilisation of the prefill. The GEMMs run two bf16 MFMA
-    passes (activation hi and lo parts) and attention runs on fp32 MFMA, so
-    the matrix-core time at peak is 2 * gemm / bf16 peak + attn / fp32 peak;
-    mfma_frac is that time over the TTFT."""
+    passes (activation hi and lo parts); attention's QK^T (half its FLOPs)
+    runs three bf16 passes (hi.hi, lo.hi, hi.lo) and its PV on fp32 MFMA, so
+    the matrix-core time at peak is (2 gemm + 1.5 attn) / bf16 peak +
+    0.5 attn / fp32 peak; mfma_frac is that time over the TTFT."""
     gemm, attn = prefill_flops(shape, args.ctx)
     out = {"tokens": args.ctx, "ttft_ms": round(prefill_s * 1e3, 2),
            "algorithmic_tflop": round((gemm + attn) / 1e12, 3),
@@ -94,9 +95,10 @@ def prefill_report(shape, args, prefill_s: float) -> dict:
     if args.token_prefill:
         out["mode"] = "token by token (reference)"
         return out
-    at_peak_s = 2 * gemm / (BF16_MFMA_PEAK_TFLOPS * 1e12) + attn / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    at_peak_s = (2 * gemm + 1.5 * attn) / (BF16_MFMA_PEAK_TFLOPS * 1e12) + 0.5 * attn / (FP32_MFMA_PEAK_TFLOPS * 1e12)
     out.update({"mode": "batched: bf16 MFMA GEMMs (int8 weights exact in bf16, fp32 block scales, "
-                        "activations as bf16 hi + lo) + fp32 MFMA flash attention",
+                        "activations as bf16 hi + lo) + flash attention (QK^T on bf16 MFMA with hi + lo "
+                        "splits of q and k, PV on fp32 MFMA)",
                 "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
                 "mfma_time_at_peak_ms": round(at_peak_s * 1e3, 3),
                 "mfma_frac": round(at_peak_s / prefill_s, 4)})

@@ -15,16 +15,19 @@
 // and for a sampled step the LM head GEMV plus k_select1/k_select2
 // (engine.ts:817-901).
 //
-// A batched prefill runs per layer the fp32-MFMA GEMMs (k_gemm), the row
-// kernels (norms, residuals, QK-norm + RoPE + KV store) and the MFMA
-// attention k_attn_pf (+ k_attn_pf_merge for long spans).
+// A batched prefill runs per layer the bf16-MFMA GEMMs (k_gemm: int8 weights
+// exact in bf16, activations split into bf16 hi + lo), the row kernels
+// (norms, residuals, QK-norm + RoPE + KV store) and the MFMA attention
+// k_attn_pf (+ k_attn_pf_merge for long spans).
 //
 // On this multi-XCD part a device-scope fence is a whole-L2 write-back, so
 // kernels never fence and never exchange data across blocks of one launch:
 // every cross-block step is a kernel boundary.
 //
-// All arithmetic is fp32 except the int8 weight payload (dequantised exactly
-// in registers) and the sampler's f64 steps, which mirror the JS host's.
+// Decode arithmetic is fp32 except the int8 weight payload (dequantised
+// exactly in registers) and the sampler's f64 steps, which mirror the JS
+// host's. The batched prefill's bf16 products use hi + lo splits of their
+// fp32 operands and accumulate in fp32.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -999,20 +1002,23 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // Block (x = key chunk, y = query tile) covers 16 prompt rows; wave h
 // computes query head h of those rows over the chunk's keys, which are
 // staged 32 rows at a time in LDS and shared by the heads (one KV head).
-// Both products run on v_mfma_f32_16x16x4f32:
-//   S^T = K Q^T  A = 16 key rows, B = Q^T. In step (t, u) lane group
-//                g = lane / 16 supplies dim 16 t + 4 g + u of key / row
-//                lane % 16; afterwards lane l holds
-//                S^T[key 16 j + 4 g + r][row l % 16] for r < 4.
-//   O += P V     the k-index runs over (j, r) so that lane l's own S^T
-//                registers are its A operand (key 16 j + 4 g + r), B = V rows;
-//                lane l holds O[row 4 g + r][16 i + l % 16] for i < 16.
+//   S^T = K Q^T  on v_mfma_f32_16x16x32_bf16 with q and k split into bf16
+//                hi + lo (k when it is staged, q once per block): per 32
+//                dims the products hi.hi, lo.hi and hi.lo, fp32 accumulate
+//                (the dropped lo.lo term is below 2^-16 |k| |q|). Operand row
+//                c of key tile j (j < 2) is key 8 (c / 4) + 4 j + c % 4, so
+//                lane l holds S^T[key 8 g + 4 j + r][row l % 16] for r < 4,
+//                g = lane / 16.
+//   O += P V     on v_mfma_f32_16x16x4f32: the k-index runs over (j, r) so
+//                that lane l's own S^T registers are its A operand (key
+//                8 g + 4 j + r), B = V rows; lane l holds
+//                O[row 4 g + r][16 i + l % 16] for i < 16.
 // Softmax statistics of row l % 16 stay online per lane: the max is reduced
 // over the four lane groups each tile, the sum once at the end. LDS rows are
 // unpadded and XOR-swizzled so that K reads (ds_read_b128, 16 keys per lane
 // group) and V reads (ds_read_b32, 4 keys x 16 dims) hit distinct banks:
-// float4 slot f of K row k sits at slot f ^ (k % 16), column d of V row k
-// at d ^ 16 ((k / 4) % 4). A query tile whose span fits one chunk writes
+// 16-byte unit u of K row k sits at u ^ ((k % 4) + 4 (k / 8)), column d of
+// V row k at d ^ 16 ((k / 8) % 4). A query tile whose span fits one chunk writes
 // O / l; otherwise every chunk leaves (m, l, O) in `part` for
 // k_attn_pf_merge.
 // ---------------------------------------------------------------------------
@@ -1027,6 +1033,13 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t* hi, uint16_t* lo) 
 }
 
 constexpr int kPfRows = 16;   // query rows per block (one MFMA tile)
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
+}
+
 constexpr int kPfKeys = 32;   // keys per LDS tile
 
 __device__ __forceinline__ int pf_key_lo(const AttnArgs& a, int pos) {
@@ -1043,7 +1056,8 @@ __device__ __forceinline__ void pf_tile_span(const AttnArgs& a, int qt, int* klo
 }
 
 __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
-  __shared__ __align__(16) float Ks[kPfKeys * kHeadDim];
+  __shared__ __align__(16) uint16_t Kh[kPfKeys * kHeadDim];
+  __shared__ __align__(16) uint16_t Kl[kPfKeys * kHeadDim];
   __shared__ __align__(16) float Vs[kPfKeys * kHeadDim];
   const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
@@ -1066,30 +1080,48 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
       if (key >= k1) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
+  // K rows as bf16 hi / lo planes (hi = bf16(k), lo = bf16(k - hi)); the
+  // 16-byte unit u of row kr sits at u ^ kswz(kr), kswz = key bits 0, 1, 3, 4,
+  // so that the 16 rows of one MFMA operand read cover all 16 bank groups
+  auto kswz = [](int kr) { return (kr & 3) | ((kr >> 3) << 2); };
   auto stage_k = [&]() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kr = 4 * i + h;
-      *(float4*)&Ks[kr * kHeadDim + 4 * (lane ^ (kr & 15))] = st[i];
+      const float4 x = st[i];
+      const bf16x4 hi = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
+      const bf16x4 lo = {(__bf16)(x.x - (float)hi[0]), (__bf16)(x.y - (float)hi[1]), (__bf16)(x.z - (float)hi[2]),
+                         (__bf16)(x.w - (float)hi[3])};
+      const int o = kr * kHeadDim + 8 * ((lane >> 1) ^ kswz(kr)) + 4 * (lane & 1);
+      *(bf16x4*)&Kh[o] = hi;
+      *(bf16x4*)&Kl[o] = lo;
     }
   };
   auto stage_v = [&]() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kr = 4 * i + h;
-      *(float4*)&Vs[kr * kHeadDim + ((4 * lane) ^ (16 * ((kr >> 2) & 3)))] = st[i];
+      *(float4*)&Vs[kr * kHeadDim + ((4 * lane) ^ (16 * ((kr >> 3) & 3)))] = st[i];
     }
   };
   fetch(a.k_cache, k0);
 
-  // q (normed + roped) of row l % 16, dims 16 t + 4 g .. +3
+  // q (normed + roped) of row l % 16, dims 32 t + 8 g .. +7, as bf16 hi / lo
   const int row = qt * kPfRows + c16;
   const bool row_ok = row < M;
   const int prow = a.pf_start + row, plo = pf_key_lo(a, prow);
-  const float* qp = a.qkv + (size_t)min(row, M - 1) * (nq * kHeadDim + 2 * kHeadDim) + min(h, nq - 1) * kHeadDim + 4 * g;
-  float4 q[16];
+  const float* qp = a.qkv + (size_t)min(row, M - 1) * (nq * kHeadDim + 2 * kHeadDim) + min(h, nq - 1) * kHeadDim + 8 * g;
+  bf16x8 qh[8], ql[8];
 #pragma unroll
-  for (int t = 0; t < 16; ++t) q[t] = *(const float4*)(qp + 16 * t);
+  for (int t = 0; t < 8; ++t) {
+    const float4 x0 = *(const float4*)(qp + 32 * t), x1 = *(const float4*)(qp + 32 * t + 4);
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qh[t][e] = (__bf16)xs[e];
+      ql[t][e] = (__bf16)(xs[e] - (float)qh[t][e]);
+    }
+  }
   stage_k();
 
   f32x4 o[16];
@@ -1103,15 +1135,20 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
     float alpha = 1.f;
     if (active) {
       f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      // S^T = K Q^T on bf16 MFMA: per 32 dims the products hi hi, lo hi and
+      // hi lo (the dropped lo lo term is below 2^-16 of |k| |q|). Operand row
+      // c16 of key tile j is key 8 (c16 / 4) + 4 j + c16 % 4, so register r of
+      // lane group g holds key 8 g + 4 j + r.
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
+      for (int t = 0; t < 8; ++t) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const float4 kk = *(const float4*)&Ks[(16 * j + c16) * kHeadDim + 4 * ((4 * t + g) ^ c16)];
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, q[t].x, s[j], 0, 0, 0);
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, q[t].y, s[j], 0, 0, 0);
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, q[t].z, s[j], 0, 0, 0);
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, q[t].w, s[j], 0, 0, 0);
+          const int kr = 8 * (c16 >> 2) + 4 * j + (c16 & 3);
+          const int o = kr * kHeadDim + 8 * ((4 * t + g) ^ c16);
+          const bf16x8 kh = lds_bf16x8(&Kh[o]), kl = lds_bf16x8(&Kl[o]);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[t], s[j], 0, 0, 0);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[t], s[j], 0, 0, 0);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[t], s[j], 0, 0, 0);
         }
       }
       // scale + causal / window mask; online softmax of row l % 16
@@ -1120,7 +1157,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = kt + 16 * j + 4 * g + r;
+          const int key = kt + 8 * g + 4 * j + r;
           const bool ok = row_ok && key < k1 && key >= plo && key <= prow;
           p[j][r] = ok ? s[j][r] * a.scale : -INFINITY;
           mx = fmaxf(mx, p[j][r]);
@@ -1158,7 +1195,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* vr = &Vs[(16 * j + 4 * g + r) * kHeadDim + c16];
+          const float* vr = &Vs[(8 * g + 4 * j + r) * kHeadDim + c16];
 #pragma unroll
           for (int i = 0; i < 16; ++i)
             o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j][r], vr[16 * (i ^ g)], o[i], 0, 0, 0);
@@ -1237,13 +1274,7 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
 // a lane group (16 rows, one 16-byte chunk) cover all banks; the next step's
 // global loads are issued before the current step's MFMAs.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kGBM = 128, kGBN = 128, kGBP = 72;
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
-  return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
-}
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
