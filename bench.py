@@ -26,7 +26,6 @@ import numpy as np  # noqa: E402
 from gemma_amd import capi, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 METRIC = "Gemma-3-1B Q8_0 bs1 decode tok/s @ctx2k; HBM GB/s as % of peak; prefill TTFT"
 
@@ -84,10 +83,9 @@ def prefill_flops(shape, m: int):
 
 def prefill_report(shape, args, prefill_s: float) -> dict:
     """TTFT and MFMA utilisation of the prefill. The GEMMs run two bf16 MFMA
-    passes (activation hi and lo parts); attention's QK^T (half its FLOPs)
-    runs three bf16 passes (hi.hi, lo.hi, hi.lo) and its PV on fp32 MFMA, so
-    the matrix-core time at peak is (2 gemm + 1.5 attn) / bf16 peak +
-    0.5 attn / fp32 peak; mfma_frac is that time over the TTFT."""
+    passes (activation hi and lo parts) and attention's QK^T and PV three
+    (hi.hi, lo.hi, hi.lo), so the matrix-core time at peak is
+    (2 gemm + 3 attn) / bf16 peak; mfma_frac is that time over the TTFT."""
     gemm, attn = prefill_flops(shape, args.ctx)
     out = {"tokens": args.ctx, "ttft_ms": round(prefill_s * 1e3, 2),
            "algorithmic_tflop": round((gemm + attn) / 1e12, 3),
@@ -95,10 +93,10 @@ def prefill_report(shape, args, prefill_s: float) -> dict:
     if args.token_prefill:
         out["mode"] = "token by token (reference)"
         return out
-    at_peak_s = (2 * gemm + 1.5 * attn) / (BF16_MFMA_PEAK_TFLOPS * 1e12) + 0.5 * attn / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    at_peak_s = (2 * gemm + 3 * attn) / (BF16_MFMA_PEAK_TFLOPS * 1e12)
     out.update({"mode": "batched: bf16 MFMA GEMMs (int8 weights exact in bf16, fp32 block scales, "
-                        "activations as bf16 hi + lo) + flash attention (QK^T on bf16 MFMA with hi + lo "
-                        "splits of q and k, PV on fp32 MFMA)",
+                        "activations as bf16 hi + lo) + flash attention on bf16 MFMA (hi + lo splits of "
+                        "q, k, p and v; three products)",
                 "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
                 "mfma_time_at_peak_ms": round(at_peak_s * 1e3, 3),
                 "mfma_frac": round(at_peak_s / prefill_s, 4)})

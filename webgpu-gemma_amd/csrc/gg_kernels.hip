@@ -1003,22 +1003,22 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // computes query head h of those rows over the chunk's keys, which are
 // staged 32 rows at a time in LDS and shared by the heads (one KV head).
 //   S^T = K Q^T  on v_mfma_f32_16x16x32_bf16 with q and k split into bf16
-//                hi + lo (k when it is staged, q once per block): per 32
-//                dims the products hi.hi, lo.hi and hi.lo, fp32 accumulate
-//                (the dropped lo.lo term is below 2^-16 |k| |q|). Operand row
+//                hi + lo (k and v when they are staged, q once per block):
+//                per 32 dims the products hi.hi, lo.hi and hi.lo, fp32
+//                accumulate (the dropped lo.lo term is below 2^-16 |k| |q|). Operand row
 //                c of key tile j (j < 2) is key 8 (c / 4) + 4 j + c % 4, so
 //                lane l holds S^T[key 8 g + 4 j + r][row l % 16] for r < 4,
 //                g = lane / 16.
-//   O += P V     on v_mfma_f32_16x16x4f32: the k-index runs over (j, r) so
-//                that lane l's own S^T registers are its A operand (key
-//                8 g + 4 j + r), B = V rows; lane l holds
-//                O[row 4 g + r][16 i + l % 16] for i < 16.
+//   O += P V     on v_mfma_f32_16x16x32_bf16, the same three products of
+//                bf16 hi + lo splits: A = P from lane l's own S^T registers
+//                (keys 8 g .. 8 g + 7 in order), B = V^T rows staged per
+//                dim; lane l holds O[row 4 g + r][16 i + l % 16] for i < 16.
 // Softmax statistics of row l % 16 stay online per lane: the max is reduced
 // over the four lane groups each tile, the sum once at the end. LDS rows are
-// unpadded and XOR-swizzled so that K reads (ds_read_b128, 16 keys per lane
-// group) and V reads (ds_read_b32, 4 keys x 16 dims) hit distinct banks:
-// 16-byte unit u of K row k sits at u ^ ((k % 4) + 4 (k / 8)), column d of
-// V row k at d ^ 16 ((k / 8) % 4). A query tile whose span fits one chunk writes
+// unpadded and XOR-swizzled so that the ds_read_b128 operand reads (16 rows
+// per lane group) hit distinct banks: 16-byte unit u of K row k sits at
+// u ^ ((k % 4) + 4 (k / 8)), unit u (keys 8u .. 8u + 7) of V^T dim row d at
+// u ^ ((d / 2) % 4). A query tile whose span fits one chunk writes
 // O / l; otherwise every chunk leaves (m, l, O) in `part` for
 // k_attn_pf_merge.
 // ---------------------------------------------------------------------------
@@ -1058,7 +1058,8 @@ __device__ __forceinline__ void pf_tile_span(const AttnArgs& a, int qt, int* klo
 __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   __shared__ __align__(16) uint16_t Kh[kPfKeys * kHeadDim];
   __shared__ __align__(16) uint16_t Kl[kPfKeys * kHeadDim];
-  __shared__ __align__(16) float Vs[kPfKeys * kHeadDim];
+  __shared__ __align__(16) uint16_t Vh[kHeadDim * kPfKeys];   // V^T: [dim][key]
+  __shared__ __align__(16) uint16_t Vl[kHeadDim * kPfKeys];
   const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.pf_rows, nq = a.n_q, qt = blockIdx.y, kc = blockIdx.x;
@@ -1068,9 +1069,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   const int k0 = klo + kc * a.pf_chunk, k1 = min(k0 + a.pf_chunk, khi + 1);
   const bool active = h < nq;
 
-  // staging: wave w moves key rows 4 i + w of a tile, lane = float4 slot.
+  // K staging: wave w moves key rows 4 i + w of a tile, lane = float4 slot.
   // V of a tile is fetched while its scores run, K of the next tile while
-  // the weighted sum runs, so 32 staging registers cover both.
+  // the weighted sum runs, so the two staging sets are never live together.
   float4 st[8];
   auto fetch = [&](const float* cache, int kt) {
 #pragma unroll
@@ -1097,11 +1098,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
       *(bf16x4*)&Kl[o] = lo;
     }
   };
-  auto stage_v = [&]() {
+  // V^T as bf16 hi / lo planes, 32 keys (64 bytes) per dim row; the 16-byte
+  // unit u (keys 8u .. 8u + 7) of dim row d sits at u ^ ((d / 2) % 4). Wave h
+  // fetches keys 8 h .. 8 h + 7, lane l dims l + 64 e, and writes unit h of
+  // its four dim rows.
+  float vv[8][4];
+  auto fetch_v = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int kr = 4 * i + h;
-      *(float4*)&Vs[kr * kHeadDim + ((4 * lane) ^ (16 * ((kr >> 3) & 3)))] = st[i];
+      const int key = kt + 8 * h + i;
+      const float* vr = a.v_cache + (size_t)(key < k1 ? key : k0) * kHeadDim + lane;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vv[i][e] = key < k1 ? vr[64 * e] : 0.f;
+    }
+  };
+  auto stage_v = [&]() {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        hi[i] = (__bf16)vv[i][e];
+        lo[i] = (__bf16)(vv[i][e] - (float)hi[i]);
+      }
+      const int d = lane + 64 * e;
+      const int o = d * kPfKeys + 8 * (h ^ ((d >> 1) & 3));
+      *(bf16x8*)&Vh[o] = hi;
+      *(bf16x8*)&Vl[o] = lo;
     }
   };
   fetch(a.k_cache, k0);
@@ -1129,7 +1152,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   for (int i = 0; i < 16; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   for (int kt = k0; kt < k1; kt += kPfKeys) {
-    fetch(a.v_cache, kt);
+    fetch_v(kt);
     __syncthreads();   // K of this tile staged; the previous tile's V reads done
     float p[2][4];
     float alpha = 1.f;
@@ -1191,15 +1214,25 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
       for (int i = 0; i < 16; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[i][r] *= ar[r];
+      // O += P V on bf16 MFMA: A = P (row l % 16, keys 8 g .. 8 g + 7 =
+      // p[j][r] for key 8 g + 4 j + r), B = V^T rows; hi.hi, lo.hi, hi.lo
+      bf16x8 ph, pl;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float* vr = &Vs[(8 * g + 4 * j + r) * kHeadDim + c16];
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[j][r], vr[16 * (i ^ g)], o[i], 0, 0, 0);
+          ph[4 * j + r] = (__bf16)p[j][r];
+          pl[4 * j + r] = (__bf16)(p[j][r] - (float)ph[4 * j + r]);
         }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 16 * i + c16;
+        const int ov = d * kPfKeys + 8 * (g ^ ((d >> 1) & 3));
+        const bf16x8 vh = lds_bf16x8(&Vh[ov]), vl = lds_bf16x8(&Vl[ov]);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vh, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vh, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vl, o[i], 0, 0, 0);
+      }
     }
     if (kt + kPfKeys < k1) stage_k();   // no K reads until the next barrier
   }
