@@ -136,14 +136,19 @@ struct Pair {
 
 // Lane `lane` of a wave loads slot `lane` of a 4352-byte item (item-planar
 // layout): four dwordx4 loads over 1024 contiguous bytes each, one dword load.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Weight items are read once per token: nontemporal loads (the `nt` bit)
+// keep them from displacing the activations, chunk partials and K/V rows
+// that the next kernels read from L2 (0.826 -> 0.789 ms per 1B token).
 __device__ __forceinline__ void load_planes(const uint8_t* item, int lane, Pair& P) {
-  const uint4* p4 = (const uint4*)item;
-  const uint4 a = p4[lane], b = p4[64 + lane], c = p4[128 + lane], d = p4[192 + lane];
+  const u32x4* p4 = (const u32x4*)item;
+  const u32x4 a = __builtin_nontemporal_load(p4 + lane), b = __builtin_nontemporal_load(p4 + 64 + lane),
+              c = __builtin_nontemporal_load(p4 + 128 + lane), d = __builtin_nontemporal_load(p4 + 192 + lane);
   P.w[0] = a.x; P.w[1] = a.y; P.w[2] = a.z; P.w[3] = a.w;
   P.w[4] = b.x; P.w[5] = b.y; P.w[6] = b.z; P.w[7] = b.w;
   P.w[8] = c.x; P.w[9] = c.y; P.w[10] = c.z; P.w[11] = c.w;
   P.w[12] = d.x; P.w[13] = d.y; P.w[14] = d.z; P.w[15] = d.w;
-  P.w[16] = ((const uint32_t*)(item + 4096))[lane];
+  P.w[16] = __builtin_nontemporal_load((const uint32_t*)(item + 4096) + lane);
 }
 
 // acc += (sum_j q0[j] x[j]) * d0 + (sum_j q1[j] x[32+j]) * d1, each block sum
@@ -1035,7 +1040,6 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t* hi, uint16_t* lo) 
 constexpr int kPfRows = 16;   // query rows per block (one MFMA tile)
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
 }
