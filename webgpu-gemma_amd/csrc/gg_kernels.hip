@@ -137,6 +137,7 @@ struct Pair {
 // Lane `lane` of a wave loads slot `lane` of a 4352-byte item (item-planar
 // layout): four dwordx4 loads over 1024 contiguous bytes each, one dword load.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Weight items are read once per token: nontemporal loads (the `nt` bit)
 // keep them from displacing the activations, chunk partials and K/V rows
 // that the next kernels read from L2 (0.826 -> 0.789 ms per 1B token).
@@ -672,19 +673,24 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 
   // loads of pass p: key rows in the score layout, value rows in the PV
   // layout; rows are clamped into the cache (positions >= t1 are masked,
-  // pos itself is substituted from LDS)
+  // pos itself is substituted from LDS). Nontemporal: each row is read by
+  // the four head blocks of its chunk (same XCD) within one launch.
   float4 kr[8], vr[8];
   auto load_k = [&](int p) {
     const int t = min(t0 + 32 * p + 8 * wv + pl, kv_last);
-    const float4* kp = (const float4*)(a.k_cache + (size_t)t * kHeadDim);
+    const f32x4* kp = (const f32x4*)(a.k_cache + (size_t)t * kHeadDim);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kr[j] = kp[oc + 8 * j];
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 v = __builtin_nontemporal_load(kp + oc + 8 * j);
+      kr[j] = make_float4(v.x, v.y, v.z, v.w);
+    }
   };
   auto load_v = [&](int p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int t = min(t0 + 32 * p + 8 * wv + i, kv_last);
-      vr[i] = *(const float4*)(a.v_cache + (size_t)t * kHeadDim + 4 * lane);
+      const f32x4 v = __builtin_nontemporal_load((const f32x4*)(a.v_cache + (size_t)t * kHeadDim) + lane);
+      vr[i] = make_float4(v.x, v.y, v.z, v.w);
     }
   };
   // this position's RoPE row, then the first pass of K / V rows (the norm
@@ -1027,7 +1033,6 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // O / l; otherwise every chunk leaves (m, l, O) in `part` for
 // k_attn_pf_merge.
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // x = hi + lo + e with hi = bf16(x), lo = bf16(x - hi), |e| <= 2^-17 |x|
 // (the input format of the prefill GEMMs).
