@@ -166,6 +166,7 @@ def probe_kernel(shape, tensors, prompt, args):
         if had is None:
             del os.environ["GG_NO_GRAPH"]
     e.prefill(prompt, 0)
+    e.set_timing(True)   # same event traffic per step as the device-time loop
     tok = e.select()
     pos = args.ctx
     for _ in range(4):
@@ -188,7 +189,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=2048, help="context positions filled before decoding")
     ap.add_argument("--probe", default="gate_up", choices=["none", "qkv", "o", "gate_up", "down", "lm_head"])
-    ap.add_argument("--probe-layer", type=int, default=0)
+    ap.add_argument("--probe-layer", type=int, default=13,
+                    help="layer of the probed kernel: deep enough into the step that the host has queued it before the GPU gets there")
     ap.add_argument("--probe-steps", type=int, default=64, help="timed steps of the kernel-timing loop")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -205,7 +207,7 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
-    ctx_len = max(4096, args.ctx + args.warmup + args.steps + 8)
+    ctx_len = max(4096, args.ctx + args.warmup + args.steps + min(args.steps, 64) + 8)
     shape = synth.GEMMA3_1B.with_ctx(ctx_len)
     shape = shape.reference_mode() if args.reference_mode else shape.gemma3_mode()
     t0 = time.perf_counter()
@@ -234,18 +236,25 @@ def main():
         tok = e.step(tok, pos)
         pos += 1
     pos_timed0 = pos
-    fwd_ms = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
         tok = e.step(tok, pos)
-        fwd_ms.append(sum(e.last_timing()))
         pos += 1
     elapsed = time.perf_counter() - t0
+    pos_timed1 = pos
+    # device time per step from the engine's step events, in a separate
+    # untimed loop (the three event records cost ~9 us of device time a step)
+    e.set_timing(True)
+    fwd_ms = []
+    for _ in range(min(args.steps, 64)):
+        tok = e.step(tok, pos)
+        fwd_ms.append(sum(e.last_timing()))
+        pos += 1
     e.close()
 
     value = args.steps / elapsed
     ms_per_step = elapsed * 1e3 / args.steps
-    avg_bytes = float(np.mean([step_bytes(shape, p) for p in range(pos_timed0, pos)]))
+    avg_bytes = float(np.mean([step_bytes(shape, p) for p in range(pos_timed0, pos_timed1)]))
     dev_ms = float(np.mean(fwd_ms))
 
     # dominant-kernel timing: the same forward pass with its kernels launched
@@ -275,7 +284,7 @@ def main():
         "config": {"workload": "gemma3-1b-q8_0-greedy-decode-after-2048", "ctx_prefilled": args.ctx,
                    "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
                    "gemma3 (22 local layers window 512 theta 1e4, 4 global theta 1e6)",
-                   "positions": [pos_timed0, pos - 1]},
+                   "positions": [pos_timed0, pos_timed1 - 1]},
         "roofline": {"bound": "hbm", "kernel": f"{args.probe} GEMV (layer {args.probe_layer})",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),

@@ -129,8 +129,13 @@ int gg_reset_kv(gg_ctx* ctx);
 /* Parity checkpoints (debug.html readBackBuffer, 2636-2648). Synchronous. */
 int gg_read(gg_ctx* ctx, int32_t what, int32_t layer, void* dst, size_t nbytes);
 
-/* Device time of the last gg_step / gg_select, split into forward and select
- * (hipEvent timestamps recorded on the context's stream), in milliseconds. */
+/* Per-step device timing, off by default. With on != 0 every gg_step /
+ * gg_select records three HIP events on the context's stream (about 9 us of
+ * device time per step on MI355X), and gg_last_timing returns the last
+ * call's forward and select time in milliseconds (GG_ERR_INVALID when timing
+ * is off or no call has run since it was turned on). No counterpart in the
+ * reference (WebGPU timestamp queries are not used in src/). */
+int gg_set_timing(gg_ctx* ctx, int32_t on);
 int gg_last_timing(gg_ctx* ctx, float* forward_ms, float* select_ms);
 
 /* Probe: before gg_finalize, name one kernel launch of the captured graphs

@@ -119,7 +119,8 @@ struct gg_ctx {
   int probe_kind = GG_PROBE_NONE, probe_layer = 0;
   hipEvent_t probe_ev[4] = {nullptr, nullptr, nullptr, nullptr};   // kernel bracket [0, 1], empty bracket [2, 3]
   bool probe_done = false;
-  bool finalized = false, lost = false, timed = false;
+  bool finalized = false, lost = false, timed = false, probed = false;
+  bool step_timing = false;   // gg_set_timing: event records around each step
   bool use_graphs = true;   // GG_NO_GRAPH=1: launch the same kernels directly (profilers)
   std::vector<void*> allocs;
   std::string err;
@@ -812,11 +813,11 @@ int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
       const int M = std::min(c->pf_M, n - s0);
       GG_TRY(prefill_slice(c, c->tokens + s0, M, start_pos + s0));
     }
-    c->timed = false;
+    c->timed = c->probed = false;
     return sync(c, "prefill");
   }
   for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
-  c->timed = false;
+  c->timed = c->probed = false;
   return sync(c, "prefill");
 }
 
@@ -825,20 +826,22 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   c->h_st->top_p = s->top_p;
   c->h_st->rep_penalty = s->rep_penalty;
   c->h_st->u = u;
+  const bool ev = c->step_timing;   // three event records cost ~9 us of device time per step
   if (with_forward) {
     GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
-    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+    if (ev) GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
     GG_TRY(run_forward(c));
   } else {
     GG_TRY(push_state(c, offsetof(DevState, temperature), offsetof(DevState, seen_count)));
-    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+    if (ev) GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
   }
-  GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
+  if (ev) GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
   GG_TRY(run_select(c));
-  GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
+  if (ev) GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
   // the selector stores the token straight into the mapped host word
   GG_TRY(sync(c, with_forward ? "step" : "select"));
-  c->timed = true;
+  c->timed = ev;
+  c->probed = true;
   *out = c->h_out[0];
   return GG_OK;
 }
@@ -918,9 +921,16 @@ int gg_read(gg_ctx* c, int32_t what, int32_t layer, void* dst, size_t nbytes) {
   return GG_OK;
 }
 
+int gg_set_timing(gg_ctx* c, int32_t on) {
+  GG_TRY(check_ready(c));
+  c->step_timing = on != 0;
+  c->timed = false;
+  return GG_OK;
+}
+
 int gg_last_timing(gg_ctx* c, float* forward_ms, float* select_ms) {
   GG_TRY(check_ready(c));
-  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet (gg_set_timing off, or no step since)");
   float a = 0.f, b = 0.f;
   GG_HIP(c, hipEventElapsedTime(&a, c->ev[0], c->ev[1]));
   GG_HIP(c, hipEventElapsedTime(&b, c->ev[1], c->ev[2]));
@@ -942,14 +952,14 @@ int gg_set_probe(gg_ctx* c, int32_t kind, int32_t layer) {
 int gg_probe_elapsed(gg_ctx* c, float* ms) {
   GG_TRY(check_ready(c));
   if (c->probe_kind == GG_PROBE_NONE || !ms) return set_err(c, GG_ERR_INVALID, "no probe set");
-  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  if (!c->probed) return set_err(c, GG_ERR_INVALID, "no step yet");
   GG_HIP(c, hipEventElapsedTime(ms, c->probe_ev[0], c->probe_ev[1]));
   return GG_OK;
 }
 int gg_probe_overhead(gg_ctx* c, float* ms) {
   GG_TRY(check_ready(c));
   if (c->probe_kind == GG_PROBE_NONE || !ms) return set_err(c, GG_ERR_INVALID, "no probe set");
-  if (!c->timed) return set_err(c, GG_ERR_INVALID, "no timed step yet");
+  if (!c->probed) return set_err(c, GG_ERR_INVALID, "no step yet");
   GG_HIP(c, hipEventElapsedTime(ms, c->probe_ev[2], c->probe_ev[3]));
   return GG_OK;
 }

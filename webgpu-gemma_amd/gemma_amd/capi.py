@@ -92,6 +92,7 @@ _SIGS = {
     "gg_penalty_add": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int32]),
     "gg_reset_kv": (ctypes.c_int, [_P]),
     "gg_read": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32, _P, ctypes.c_size_t]),
+    "gg_set_timing": (ctypes.c_int, [_P, ctypes.c_int32]),
     "gg_last_timing": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]),
     "gg_set_probe": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32]),
     "gg_probe_elapsed": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
@@ -209,6 +210,9 @@ class Engine:
     def topk256(self):
         raw = self.read(READ_TOPK256, dtype=np.uint32)
         return raw[0::2].view(np.float32).copy(), raw[1::2].copy()
+
+    def set_timing(self, on: bool):
+        _check(self.ctx, lib().gg_set_timing(self.ctx, 1 if on else 0))
 
     def last_timing(self):
         a, b = ctypes.c_float(), ctypes.c_float()
