@@ -115,6 +115,7 @@ struct gg_ctx {
   int32_t* d_out = nullptr;           // h_out's device address
 
   hipGraphExec_t g_fwd = nullptr, g_sel = nullptr;
+  hipGraphExec_t g_step = nullptr;   // state upload + forward + select: one launch per gg_step
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int probe_kind = GG_PROBE_NONE, probe_layer = 0;
   hipEvent_t probe_ev[4] = {nullptr, nullptr, nullptr, nullptr};   // kernel bracket [0, 1], empty bracket [2, 3]
@@ -338,6 +339,17 @@ int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
   (void)hipGraphDestroy(g);
   if (e != hipSuccess) return hip_fail(c, e, "hipGraphInstantiate");
   return GG_OK;
+}
+
+int push_state(gg_ctx* c, size_t from, size_t to);
+
+// One decode step as a single graph: the DevState upload (a memcpy node
+// that reads the pinned host copy when the graph runs), the forward pass and
+// the selection.
+int record_step(gg_ctx* c) {
+  GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
+  GG_TRY(record_forward(c));
+  return record_select(c);
 }
 
 int run_forward(gg_ctx* c) {
@@ -790,6 +802,7 @@ int gg_finalize(gg_ctx* c) {
   if (c->use_graphs) {
     GG_TRY(capture(c, record_forward, &c->g_fwd));
     GG_TRY(capture(c, record_select, &c->g_sel));
+    GG_TRY(capture(c, record_step, &c->g_step));
   }
   c->finalized = true;
   return GG_OK;
@@ -827,6 +840,14 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   c->h_st->rep_penalty = s->rep_penalty;
   c->h_st->u = u;
   const bool ev = c->step_timing;   // three event records cost ~9 us of device time per step
+  if (with_forward && !ev && c->use_graphs) {
+    GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
+    GG_TRY(sync(c, "step"));
+    c->timed = false;
+    c->probed = true;
+    *out = c->h_out[0];
+    return GG_OK;
+  }
   if (with_forward) {
     GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
     if (ev) GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
@@ -971,6 +992,7 @@ void gg_destroy(gg_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
   if (c->g_sel) (void)hipGraphExecDestroy(c->g_sel);
+  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
   for (hipEvent_t e : c->ev)
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->probe_ev)
