@@ -393,11 +393,17 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
   const int wi0 = i0 + (wv * ni) / W, wi1 = i0 + ((wv + 1) * ni) / W;
   const int K4 = K / 4;   // thread t owns the float4 chunks t + NT i (i < EPT) of x
 
+  // Lanes of a padding column phase (c >= Kp, the tail item of a row group
+  // when Kp % CI != 0) load the phase-0 lane of their row instead: the same
+  // cache lines, so the padding bytes are not fetched (their products are
+  // masked below).
   auto issue_weights = [&](Pair* w) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < NIF; ++k) {
       const int it = max(min(wi0 + k, wi1 - 1), i0);
-      load_planes(a.W + (size_t)it * kColBytes, lane, w[k]);
+      const int sp = it % KpS;
+      const int ll = sp * CI + cp < Kp ? lane : (lane & (GR - 1));
+      load_planes(a.W + (size_t)it * kColBytes, ll, w[k]);
     }
   };
   Pair st[NIF];
