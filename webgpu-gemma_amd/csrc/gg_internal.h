@@ -106,7 +106,9 @@ struct GemvArgs {
   // decode attention chunk partials of this token
   const float* attn_part;  // o [kDecMaxChunks][kAttnMaxQ][256], then (m, l) [kDecMaxChunks][kAttnMaxQ][2]
   int attn_chunks;         // chunks the attention launch wrote (blocks past the span leave empty ones)
-  float* x_out;            // block 0 stores the merged x here (the attention output)
+  float* x_out;            // block 0 stores the merged x here (the attention output; for the
+                           // LM head with PRO_RESID_NORM: the normed hidden state)
+  DevState* st_advance;    // LM head with the final norm fused: block 0 advances pos / cursor
 };
 
 struct AttnArgs {

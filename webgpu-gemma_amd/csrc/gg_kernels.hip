@@ -278,7 +278,16 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
   const float rms = sqrtf(block_sum256(ss, sh4) / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
 #pragma unroll
   for (int i = 0; i < kMaxEPT / 4; ++i)
-    if (i < n) xs[xs_index(tid + 256 * i)] = (r[i] * wp[i]) / rms;
+    if (i < n) {
+      const float x = (r[i] * wp[i]) / rms;
+      xs[xs_index(tid + 256 * i)] = x;
+      if (PRO == PRO_RESID_NORM && blockIdx.x == 0 && a.x_out) a.x_out[tid + 256 * i] = x;
+    }
+  // the LM head carrying k_final's work also carries its step of the state
+  if (PRO == PRO_RESID_NORM && blockIdx.x == 0 && tid == 0 && a.st_advance) {
+    a.st_advance->pos += 1;
+    a.st_advance->cursor += 1;
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -211,7 +211,9 @@ GemvArgs gemv_base(const uint8_t* W, const Q8Layout& L, float* out) {
 }
 
 // Record the forward pass of one token (engine.ts:735-802).
-int record_forward(gg_ctx* c) {
+// `final_norm` false: stop after the last down GEMV; the LM head then
+// carries k_final's work (record_select_impl with fused_final).
+int record_forward_impl(gg_ctx* c, bool final_norm) {
   const float eps = c->c.rms_norm_eps;
   for (int l = 0; l < c->L; ++l) {
     Layer& Ly = c->layers[l];
@@ -289,6 +291,7 @@ int record_forward(gg_ctx* c) {
       GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_down.CI, d, c->stream), "down gemv"));
     }
   }
+  if (!final_norm) return GG_OK;
   FinalArgs f{};
   f.pre_vec = c->down_out;
   f.pre_res = c->residual;
@@ -303,13 +306,30 @@ int record_forward(gg_ctx* c) {
   return launch_rc(c, launch_final(f, c->stream), "final norm");
 }
 
-// Record LM head + selection (engine.ts:805-902).
-int record_select(gg_ctx* c) {
+int record_forward(gg_ctx* c) { return record_forward_impl(c, true); }
+
+// Record LM head + selection (engine.ts:805-902). With `fused_final` the LM
+// head's prologue does k_final's work (post-FFN norm + residual, output norm,
+// hidden / normed / history stores and the position step, engine.ts:794-801)
+// from the last down GEMV's output: one launch fewer per decode step.
+int record_select_impl(gg_ctx* c, bool fused_final) {
   GemvArgs lm = gemv_base(c->embd, c->lay_embd, c->logits);
   lm.x = c->normed;
+  if (fused_final) {
+    lm.pre_vec = c->down_out;
+    lm.pre_res = c->residual;
+    lm.w_post = c->layers[c->L - 1].norm[N_POST_FFW];
+    lm.w_pre = c->out_norm;
+    lm.res_out = c->hidden;
+    lm.hist_out = c->hist + (size_t)(c->L - 1) * c->H;
+    lm.x_out = c->normed;
+    lm.st_advance = c->st;
+    lm.eps = c->c.rms_norm_eps;
+  }
   {
     ProbeScope ps(c, GG_PROBE_LM_HEAD, -1);
-    GG_TRY(launch_rc(c, launch_gemv(PRO_NONE, EPI_OUT, c->lay_embd.CI, lm, c->stream), "lm head"));
+    GG_TRY(launch_rc(c, launch_gemv(fused_final ? PRO_RESID_NORM : PRO_NONE, EPI_OUT, c->lay_embd.CI, lm, c->stream),
+                     "lm head"));
   }
   SelectArgs s{};
   s.logits = c->logits;
@@ -324,6 +344,8 @@ int record_select(gg_ctx* c) {
   ProbeScope ps(c, GG_PROBE_SELECT, -1);
   return launch_rc(c, launch_select(s, c->stream), "select");
 }
+
+int record_select(gg_ctx* c) { return record_select_impl(c, false); }
 
 int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
   GG_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
@@ -348,8 +370,8 @@ int push_state(gg_ctx* c, size_t from, size_t to);
 // the selection.
 int record_step(gg_ctx* c) {
   GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
-  GG_TRY(record_forward(c));
-  return record_select(c);
+  GG_TRY(record_forward_impl(c, false));
+  return record_select_impl(c, true);
 }
 
 int run_forward(gg_ctx* c) {
@@ -840,8 +862,9 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   c->h_st->rep_penalty = s->rep_penalty;
   c->h_st->u = u;
   const bool ev = c->step_timing;   // three event records cost ~9 us of device time per step
-  if (with_forward && !ev && c->use_graphs) {
-    GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
+  if (with_forward && !ev) {
+    if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
+    else GG_TRY(record_step(c));
     GG_TRY(sync(c, "step"));
     c->timed = false;
     c->probed = true;
