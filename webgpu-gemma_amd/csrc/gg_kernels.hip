@@ -1484,14 +1484,24 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
   const int row = blockIdx.x, tid = threadIdx.x, H = a.H;
   const int n = (H - tid + 255) / 256;
   const size_t o = (size_t)row * H;
-  float v[8], rs[8], wq[8];
+  float v[8], rs[8], wq[8], pv[kGemmMaxSlices - 1][8];
+  // every plane's loads are issued before the sums (planes of a K split)
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
       v[i] = a.pre[o + tid + 256 * i];
-      for (int p = 1; p < a.pre_planes; ++p) v[i] += a.pre[p * a.pre_stride + o + tid + 256 * i];
+#pragma unroll
+      for (int p = 1; p < kGemmMaxSlices; ++p)
+        if (p < a.pre_planes) pv[p - 1][i] = a.pre[p * a.pre_stride + o + tid + 256 * i];
       rs[i] = a.res[o + tid + 256 * i];
       wq[i] = a.w_post[tid + 256 * i];
+    }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < n) {
+#pragma unroll
+      for (int p = 1; p < kGemmMaxSlices; ++p)
+        if (p < a.pre_planes) v[i] += pv[p - 1][i];
     }
   float s1 = 0.f;
 #pragma unroll
