@@ -271,3 +271,38 @@ def test_1b_32k_three_turns_sampling(gpu):
     assert b.step(tok, pos, *opts, u) == nxt
     assert np.array_equal(b.read(capi.READ_LOGITS), logits)
     b.close()
+
+
+def test_step_timing_opt_in_and_fused_final(gpu, tiny_model):
+    """gg_set_timing: gg_last_timing fails while timing is off and returns the
+    step's device times while it is on. The timed step runs the forward graph
+    with k_final and the plain LM head; the untimed step runs the step graph,
+    whose LM head prologue does k_final's work: both give the same logits,
+    hidden state and tokens bit for bit."""
+    shape = synth.TINY.gemma3_mode(window=7)
+    say("step timing + fused final norm")
+    a, b = engine(shape, tiny_model), engine(shape, tiny_model)
+    prompt = synth.prompt_ids(9, seed=11, vocab=shape.vocab)
+    for e in (a, b):
+        e.prefill(prompt, 0)
+    ta, tb = a.select(), b.select()
+    assert ta == tb
+    b.set_timing(True)
+    pos = len(prompt)
+    for step in range(6):
+        ta = a.step(ta, pos)
+        with pytest.raises(capi.GGError):
+            a.last_timing()
+        tb = b.step(tb, pos)
+        fwd, sel = b.last_timing()
+        assert fwd > 0.0 and sel > 0.0
+        assert ta == tb, f"step {step}"
+        for what in (capi.READ_LOGITS, capi.READ_HIDDEN, capi.READ_NORMED):
+            assert np.array_equal(a.read(what), b.read(what)), f"step {step} read {what}"
+        pos += 1
+    b.set_timing(False)
+    tb = b.step(tb, pos)
+    with pytest.raises(capi.GGError):
+        b.last_timing()
+    a.close()
+    b.close()
