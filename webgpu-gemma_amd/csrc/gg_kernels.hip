@@ -1326,19 +1326,28 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
 // added to the output in fp32 -- the linearQ8 structure (shaders.ts:123-142)
 // with the block sum on the matrix cores.
 //
-// Block tile 128 (rows) x 128 (features) x 64 (k step), four waves of 64 x 64
-// (4 x 4 MFMA tiles). LDS rows are padded to 72 bf16 so that the 16 lanes of
-// a lane group (16 rows, one 16-byte chunk) cover all banks; the next step's
-// global loads are issued before the current step's MFMAs.
+// Block tile 128 (rows) x BN (features) x 64 (k step), four waves of
+// 16 NI x 16 NJ (NI x NJ MFMA tiles): 2 x 2 waves of 64 x 64 (BN = 128) or
+// 4 x 1 waves of 32 x 144 (BN = 144; 1152-wide outputs then split into 8
+// tiles, so that a K split of 4 fills the 512 block slots of the chip
+// exactly). LDS rows are padded to 72 bf16 so that the 16 lanes of a lane
+// group (16 rows, one 16-byte chunk) cover all banks; the next step's global
+// loads are issued before the current step's MFMAs.
 // ---------------------------------------------------------------------------
-constexpr int kGBM = 128, kGBN = 128, kGBP = 72;
+constexpr int kGBM = 128, kGBP = 72;
 
-template <int EPI>
+template <int EPI, int NI, int NJ>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
+  constexpr int WM = 128 / (16 * NI), WN = 4 / WM;   // waves along rows / features
+  constexpr int BN = WN * 16 * NJ;
+  constexpr int WI = (BN * 8 + 255) / 256;   // 16-byte W chunks per thread and step
+  constexpr int DI = (BN * 2 + 255) / 256;   // block scales per thread and step
+  static_assert(WM * WN == 4 && WM * 16 * NI == kGBM, "four waves cover the 128-row tile");
+  static_assert(EPI == EPI_OUT || NJ % 2 == 0, "GeGLU pairs adjacent column tiles");
   __shared__ __align__(16) uint16_t Ah[kGBM * kGBP];
   __shared__ __align__(16) uint16_t Al[kGBM * kGBP];
-  __shared__ __align__(16) uint16_t Ws[kGBN * kGBP];
-  __shared__ float Ds[kGBN * 2];
+  __shared__ __align__(16) uint16_t Ws[BN * kGBP];
+  __shared__ float Ds[BN * 2];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.M, K = a.K;
@@ -1351,27 +1360,31 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   const int L = (G % 8 == 0) ? (bid % 8) * (G / 8) + bid / 8 : bid;
   const int kz = L / (NT * MT), Lp = L % (NT * MT);
   const int fm = (Lp / (4 * NT)) * 4, gm = min(MT - fm, 4);
-  const int m0 = (fm + (Lp % (4 * NT)) % gm) * kGBM, n0 = ((Lp % (4 * NT)) / gm) * kGBN;
+  const int m0 = (fm + (Lp % (4 * NT)) % gm) * kGBM, n0 = ((Lp % (4 * NT)) / gm) * BN;
   const int kn = K / a.ks;   // this block's K slice [kz kn, (kz + 1) kn)
-  const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
+  const int wm = (wv / WN) * 16 * NI, wn = (wv % WN) * 16 * NJ;
   const size_t MK = (size_t)M * K;
   // staging: rows tid / 8 + 32 i, 16-byte chunk tid % 8 of the 64-wide step;
-  // scale (row tid / 2, block tid % 2)
+  // scale (row tid / 2 + 128 i, block tid % 2)
   const int sr = tid >> 3, sc = (tid & 7) * 8;
   const uint16_t* a0 = a.A + sc;
   const uint16_t* w0 = a.W + (size_t)(n0 + sr) * K + sc;
   const float* dp = a.D + (size_t)(n0 + (tid >> 1)) * (K / 32) + (tid & 1);
-  u32x4 rh[4], rl[4], rw[4];
-  float rd;
+  u32x4 rh[4], rl[4], rw[WI];
+  float rd[DI];
   auto fetch = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint16_t* ar = a0 + (size_t)min(m0 + sr + 32 * i, M - 1) * K + k0;
       rh[i] = *(const u32x4*)ar;
       rl[i] = *(const u32x4*)(ar + MK);
-      rw[i] = *(const u32x4*)(w0 + (size_t)(32 * i) * K + k0);
     }
-    rd = dp[k0 / 32];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+      if (BN >= 32 * (i + 1) || sr + 32 * i < BN) rw[i] = *(const u32x4*)(w0 + (size_t)(32 * i) * K + k0);
+#pragma unroll
+    for (int i = 0; i < DI; ++i)
+      if (BN >= 128 * (i + 1) || tid + 256 * i < 2 * BN) rd[i] = dp[(size_t)(128 * i) * (K / 32) + k0 / 32];
   };
   auto stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -1379,16 +1392,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
       const int r = (sr + 32 * i) * kGBP + sc;
       *(u32x4*)&Ah[r] = rh[i];
       *(u32x4*)&Al[r] = rl[i];
-      *(u32x4*)&Ws[r] = rw[i];
     }
-    Ds[tid] = rd;
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+      if (BN >= 32 * (i + 1) || sr + 32 * i < BN) *(u32x4*)&Ws[(sr + 32 * i) * kGBP + sc] = rw[i];
+#pragma unroll
+    for (int i = 0; i < DI; ++i)
+      if (BN >= 128 * (i + 1) || tid + 256 * i < 2 * BN) Ds[tid + 256 * i] = rd[i];
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[NI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int kb = kz * kn, ke = kb + kn;
   fetch(kb);
   for (int k0 = kb; k0 < ke; k0 += 64) {
@@ -1398,23 +1415,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     if (k0 + 64 < ke) fetch(k0 + 64);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      bf16x8 xh[4], xl[4], w[4];
-      float d[4];
+      bf16x8 xh[NI], xl[NI], w[NJ];
+      float d[NJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NI; ++i) {
         const int o = (wm + 16 * i + c16) * kGBP + 32 * b + 8 * g;
         xh[i] = lds_bf16x8(&Ah[o]);
         xl[i] = lds_bf16x8(&Al[o]);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         w[j] = lds_bf16x8(&Ws[(wn + 16 * j + c16) * kGBP + 32 * b + 8 * g]);
         d[j] = Ds[(wn + 16 * j + c16) * 2 + b];
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh[i], w[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl[i], w[j], p, 0, 0, 0);
 #pragma unroll
@@ -1425,13 +1442,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   // D[i][j] of a 16x16 tile: lane l, register r -> row 4 (l / 16) + r, col l % 16
   const size_t half_plane = (size_t)M * (a.N / 2);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + wm + 16 * i + 4 * g + r;
       if (m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int n = n0 + wn + 16 * j + c16;
         if (EPI == EPI_OUT) {
           a.C[(size_t)kz * M * a.N + (size_t)m * a.N + n] = acc[i][j][r];
@@ -1790,12 +1807,15 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
 }
 
 int launch_gemm(int epi, const GemmArgs& a, void* stream) {
-  if (a.M < 1 || a.N < kGBN || a.N % kGBN || a.K < 64 || a.ks < 1 || a.ks > kGemmMaxSlices || a.K % (64 * a.ks) ||
-      !a.A || !a.W || !a.D || (epi == EPI_OUT ? !a.C : (!a.act || a.ks != 1)))
+  const int bn = a.bn;
+  if (a.M < 1 || (bn != 128 && bn != 144) || (bn == 144 && epi != EPI_OUT) || a.N < bn || a.N % bn ||
+      a.K < 64 || a.ks < 1 || a.ks > kGemmMaxSlices || a.K % (64 * a.ks) || !a.A || !a.W || !a.D ||
+      (epi == EPI_OUT ? !a.C : (!a.act || a.ks != 1)))
     return (int)hipErrorInvalidValue;
-  dim3 grid(a.N / kGBN, (a.M + kGBM - 1) / kGBM, a.ks);
-  if (epi == EPI_OUT) hipLaunchKernelGGL(k_gemm<EPI_OUT>, grid, dim3(256), 0, (hipStream_t)stream, a);
-  else hipLaunchKernelGGL(k_gemm<EPI_GEGLU>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  dim3 grid(a.N / bn, (a.M + kGBM - 1) / kGBM, a.ks);
+  if (epi == EPI_GEGLU) hipLaunchKernelGGL((k_gemm<EPI_GEGLU, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, a);
+  else if (bn == 128) hipLaunchKernelGGL((k_gemm<EPI_OUT, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL((k_gemm<EPI_OUT, 2, 9>), grid, dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

@@ -400,21 +400,36 @@ int sync(gg_ctx* c, const char* what) {
 }
 
 
-// K slices (up to max_ks, dividing K into whole 64-steps) that minimise the
-// modelled time: steps per block times the load of the busiest CU, where n >= 2
-// co-resident blocks take 0.75 n of one block's time (measured on the 1B down
-// GEMM: 144 blocks x 108 steps 165 us, 288 x 54 124 us). C must hold that many
-// slices; the consumer adds them.
-int gemm_slices(int N, int K, int M, int max_ks) {
-  const int tiles = (N / 128) * ((M + 127) / 128), steps = K / 64;
-  auto cost = [&](int ks) {
-    const int per_cu = (tiles * ks + 255) / 256;
-    return (per_cu == 1 ? 1.0 : 0.75 * per_cu) * (steps / ks);
-  };
-  int best = 1;
-  for (int ks = 2; ks <= max_ks; ++ks)
-    if (steps % ks == 0 && cost(ks) < cost(best)) best = ks;
-  return best;
+// Block tile width (128, or 144 for a C output whose width it divides) and K
+// slices (up to max_ks, dividing K into whole 64-steps) that minimise the
+// modelled time, in units of one block's 64-wide step on a CU of its own:
+// steps per block times the load of the busiest CU, where n >= 2 co-resident
+// blocks take 0.75 n of one block's time (measured on the 1B down GEMM: 144
+// blocks x 108 steps 165 us, 288 x 54 124 us), times 1.2 for the 144-wide
+// tile (1.125x the work per step; 85.5 us for 512 x 27 steps against 98.6 us
+// for 432 x 36 steps of the 128-wide tile), plus one unit per 2.29 M outputs
+// of each slice for the consumer's read of that slice (9.4 MB in ~1.9 us at
+// M = 2048, N = 1152). C must hold that many slices; the consumer adds them.
+void gemm_plan(int N, int K, int M, int max_ks, bool out, int* bn_out, int* ks_out) {
+  const int steps = K / 64;
+  double best_cost = 0.0;
+  *bn_out = 128;
+  *ks_out = 1;
+  for (int bn : {128, 144}) {
+    if (N % bn || (bn == 144 && !out)) continue;
+    const int tiles = (N / bn) * ((M + 127) / 128);
+    for (int ks = 1; ks <= max_ks; ++ks) {
+      if (steps % ks) continue;
+      const int per_cu = (tiles * ks + 255) / 256;
+      const double cost = (per_cu == 1 ? 1.0 : 0.75 * per_cu) * (steps / ks) * (bn == 144 ? 1.2 : 1.0) +
+                          (out ? ks * ((double)M * N / 2.29e6) : 0.0);
+      if ((bn == 128 && ks == 1) || cost < best_cost) {
+        best_cost = cost;
+        *bn_out = bn;
+        *ks_out = ks;
+      }
+    }
+  }
 }
 
 GemmArgs gemm_base(const uint16_t* A, const uint16_t* W, const float* D, int N, int K, int M, float* C,
@@ -428,7 +443,7 @@ GemmArgs gemm_base(const uint16_t* A, const uint16_t* W, const float* D, int N, 
   g.K = K;
   g.C = C;
   g.act = act;
-  g.ks = C ? gemm_slices(N, K, M, max_ks) : 1;
+  gemm_plan(N, K, M, C ? max_ks : 1, C != nullptr, &g.bn, &g.ks);
   return g;
 }
 
@@ -480,7 +495,7 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     at.pf_rows = M;
     at.pf_chunk = prefill_chunk(at.window, start, M);
     GG_TRY(launch_rc(c, launch_prefill_attention(at, M, s), "prefill attention"));
-    const GemmArgs go = gemm_base(c->pf_attn, Ly.o_b, Ly.o_d, c->H, c->QD, M, c->pf_o, nullptr, 2);
+    const GemmArgs go = gemm_base(c->pf_attn, Ly.o_b, Ly.o_d, c->H, c->QD, M, c->pf_o, nullptr, kGemmMaxSlices);
     GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, go, s), "prefill o"));
     RowArgs r1 = r;
     r1.pre = c->pf_o;
@@ -493,7 +508,7 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
     r1.x_out = c->pf_xn;
     GG_TRY(launch_rc(c, launch_rows_resid(r1, s), "prefill post-attn"));
     GG_TRY(launch_rc(c, launch_gemm(EPI_GEGLU, gemm_base(c->pf_xn, Ly.gu_b, Ly.gu_d, 2 * c->I, c->H, M, nullptr, c->pf_act), s), "prefill gate/up"));
-    const GemmArgs gd = gemm_base(c->pf_act, Ly.down_b, Ly.down_d, c->H, c->I, M, c->pf_o, nullptr, 3);
+    const GemmArgs gd = gemm_base(c->pf_act, Ly.down_b, Ly.down_d, c->H, c->I, M, c->pf_o, nullptr, kGemmMaxSlices);
     GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gd, s), "prefill down"));
     if (l + 1 < c->L) {
       RowArgs r2 = r;
