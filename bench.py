@@ -5,12 +5,15 @@ A "step" is one decode token: forward pass over 26 layers + tied LM head +
 greedy selection, with the token read back to the host (one gg_step call, as
 the reference's per-token loop does). Weights are seeded random-init Q8_0 of
 the 1B architecture (no checkpoint is available offline); the KV cache holds
-2048 positions from a step-by-step prefill of seeded ids before timing.
+2048 positions from a batched prefill of seeded ids before timing (--ctx
+changes the context, e.g. --ctx 32760 for the long-context case).
 
-Prints one JSON line. `roofline` covers the dominant kernel, timed inside the
-timed loop by HIP event-record nodes captured around that launch in the
-graph; `cpu_baseline` times the C oracle (a CPU restatement of the reference
-pipeline) on a bounded sample of the same decode steps.
+Prints one JSON line. `roofline` covers the dominant kernel: a second engine
+runs the same decode steps with its kernels launched directly, and HIP events
+around that kernel's launch give its mean duration. `prefill` reports the
+TTFT of the batched prefill and its matrix-core utilisation; `cpu_baseline`
+times the C oracle (a CPU restatement of the reference pipeline) on a bounded
+sample of the same decode steps.
 """
 import argparse
 import json
@@ -152,13 +155,20 @@ def cpu_baseline(shape, tensors, pos0: int, budget_s: float, threads: int):
                       f"output rows, {el:.1f} s"}
 
 
+def prefill_rows(args) -> int:
+    """Rows per batched prefill slice (0 = token by token)."""
+    if args.token_prefill:
+        return 0
+    return args.prefill_batch or min(args.ctx, 4096)
+
+
 def probe_kernel(shape, tensors, prompt, args):
     """Mean device time (ms) of the probed kernel and of an empty event pair
     over args.probe_steps decode steps whose kernels are launched directly."""
     had = os.environ.get("GG_NO_GRAPH")
     os.environ["GG_NO_GRAPH"] = "1"
     try:
-        e = capi.Engine(shape.gg_config(prefill_batch=0 if args.token_prefill else args.ctx))
+        e = capi.Engine(shape.gg_config(prefill_batch=prefill_rows(args)))
         e.set_probe(args.probe, args.probe_layer)
         e.upload_model(tensors)
         e.finalize()
@@ -197,6 +207,8 @@ def main():
     ap.add_argument("--reference-mode", action="store_true", help="full attention, one theta (src/ as shipped)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one device-to-device copy of BYTES first (PMC calibration runs)")
+    ap.add_argument("--prefill-batch", type=int, default=0,
+                    help="rows per batched prefill slice (default: the whole context, at most 4096)")
     ap.add_argument("--token-prefill", action="store_true",
                     help="fill the context token by token (the reference's prefillBatched) instead of batched")
     args = ap.parse_args()
@@ -207,13 +219,15 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
-    ctx_len = max(4096, args.ctx + args.warmup + args.steps + min(args.steps, 64) + 8)
+    # positions decoded past the context: the timed engine's warm-up, timed and
+    # device-timing steps, or the kernel-timing engine's 4 + probe_steps
+    ctx_len = max(4096, args.ctx + max(args.warmup + args.steps + min(args.steps, 64), 4 + args.probe_steps) + 8)
     shape = synth.GEMMA3_1B.with_ctx(ctx_len)
     shape = shape.reference_mode() if args.reference_mode else shape.gemma3_mode()
     t0 = time.perf_counter()
     tensors = synth.make_model(shape, seed=1)
     t_gen = time.perf_counter() - t0
-    cfg = shape.gg_config(prefill_batch=0 if args.token_prefill else args.ctx)
+    cfg = shape.gg_config(prefill_batch=prefill_rows(args))
     e = capi.Engine(cfg)
     e.upload_model(tensors)
     e.finalize()
@@ -269,7 +283,7 @@ def main():
     k_ms = bracket_ms
     achieved = k_bytes / (k_ms * 1e-3) / 1e9
     out = {
-        "metric": METRIC,
+        "metric": METRIC if args.ctx == 2048 else METRIC.replace("@ctx2k", f"@ctx{args.ctx}"),
         "value": round(value, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -281,7 +295,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded random-init Q8_0 weights of the Gemma-3-1B architecture, seeded uniform ids",
-        "config": {"workload": "gemma3-1b-q8_0-greedy-decode-after-2048", "ctx_prefilled": args.ctx,
+        "config": {"workload": f"gemma3-1b-q8_0-greedy-decode-after-{args.ctx}", "ctx_prefilled": args.ctx,
                    "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
                    "gemma3 (22 local layers window 512 theta 1e4, 4 global theta 1e6)",
                    "positions": [pos_timed0, pos_timed1 - 1]},
