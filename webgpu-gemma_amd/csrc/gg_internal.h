@@ -32,7 +32,8 @@ constexpr int kColBytes = 64 * kPairBytes;   // one wavefront step: 4352 bytes
 constexpr int kMaxK = 8192;          // largest GEMV input (x staged in LDS)
 constexpr int kSelBlocks = 32;       // stage-1 blocks of the vocab selector
 constexpr int kAttnChunk = 32;       // base positions per decode attention block (4 waves x 8)
-constexpr int kDecMaxChunks = 64;    // decode attention chunks per token (16 while the span is <= 4096)
+constexpr int kDecMaxChunks = 256;   // decode attention chunks of a long-span launch (else 16)
+constexpr int kDecMergeInO = 16;     // launches of at most this many chunks are merged by the O GEMV
 constexpr int kMaxContext = 65536;   // largest context_length
 
 // Byte offset of dword j (0..16) of slot s (0..63) inside a 4352-byte item.
@@ -213,10 +214,11 @@ enum Epilogue { EPI_OUT = 0, EPI_GEGLU = 1 };
 
 int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream);
 int launch_attention(const AttnArgs& a, int grid, void* stream);
+int launch_attention_merge(const AttnArgs& a, int chunks, void* stream);
 // Decode attention chunks of a layer: 16 while its span cannot exceed 4096
 // positions (a window <= 4096, or a context <= 4096), else kDecMaxChunks.
 inline int decode_attention_chunks(int ctx, int window) {
-  return (ctx <= 4096 || (window > 0 && window <= 4096)) ? 16 : kDecMaxChunks;
+  return (ctx <= 4096 || (window > 0 && window <= 4096)) ? kDecMergeInO : kDecMaxChunks;
 }
 int launch_final(const FinalArgs& a, void* stream);
 int launch_select(const SelectArgs& a, void* stream);

@@ -371,11 +371,11 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // the wave's LDS slots, and a fixed-order sum over the waves gives the rows
 // (deterministic). Prologue reductions run on the DPP network.
 // ---------------------------------------------------------------------------
-// Decode attention chunking (shared by k_attn_dec and the merge prologue).
-__device__ __forceinline__ void dec_span(int pos, int window, int* t_lo, int* ch, int* nch) {
+// Decode attention chunking: the span split into at most mc (the launch's
+// chunk count) chunks of a multiple of 32 positions.
+__device__ __forceinline__ void dec_span(int pos, int window, int mc, int* t_lo, int* ch, int* nch) {
   const int lo = window > 0 ? max(0, pos - window + 1) : 0;
   const int span = pos - lo + 1;
-  const int mc = span <= 4096 ? 16 : kDecMaxChunks;
   const int c = kAttnChunk * ((span + kAttnChunk * mc - 1) / (kAttnChunk * mc));
   *t_lo = lo;
   *ch = c;
@@ -646,22 +646,25 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 // Softmax statistics are kept online per pass; all reductions run on DPP,
 // probabilities reach every lane through readlane.
 // ---------------------------------------------------------------------------
+template <int HPB>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
-  __shared__ float4 qs4[64];
+  __shared__ float4 qs4[HPB][64];
   __shared__ float4 ks4[64], vs4[64];
-  __shared__ float4 wo[4][64];
-  __shared__ float wm[4], wl[4], fw[4], hst[2];
+  __shared__ float4 wo[4][HPB][64];
+  __shared__ float wm[4][HPB], wl[4][HPB], fw[4][HPB], hst[HPB][2];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
   const int nqd = nq * kHeadDim;
-  const int h = blockIdx.y;
-  // loads that do not depend on the position: q of head h, this token's k
-  // and v, the norm weights
+  const int h0 = HPB == 1 ? (int)blockIdx.y : 0;   // first query head of the block
+  // loads that do not depend on the position: q of the head this wave
+  // normalises (HPB = 1: wave 0, head h0; else wave w, head w), this token's
+  // k and v, the norm weights
+  const int qh = HPB == 1 ? h0 : min(wv, nq - 1);
   float hx[4], kx[4], nwt[4], kwt[4], cs[2], sn[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    hx[i] = a.qkv[h * kHeadDim + lane + 64 * i];
+    hx[i] = a.qkv[qh * kHeadDim + lane + 64 * i];
     nwt[i] = a.q_norm[lane + 64 * i];
     kx[i] = a.qkv[nqd + lane + 64 * i];
     kwt[i] = a.k_norm[lane + 64 * i];
@@ -669,13 +672,18 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
   const float4 vme = *(const float4*)(a.qkv + nqd + kHeadDim + 4 * lane);
   const int pos = a.st->pos;
   int t_lo, ch, nch;
-  dec_span(pos, a.window, &t_lo, &ch, &nch);
+  dec_span(pos, a.window, gridDim.x, &t_lo, &ch, &nch);
   const int b = blockIdx.x;
-  if (b >= nch) {   // past the span: an empty partial, so that the merge needs no position
-    if (tid < 64) *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid == 0) {
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = -INFINITY;
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = 0.f;
+  if (b >= nch) {   // past the span: empty partials, so that the merge needs no position
+#pragma unroll
+    for (int hh = 0; hh < HPB; ++hh) {
+      const int h = h0 + hh;
+      if (h >= nq) break;
+      if (tid < 64) *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tid == 0) {
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = -INFINITY;
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = 0.f;
+      }
     }
     return;
   }
@@ -688,8 +696,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 
   // loads of pass p: key rows in the score layout, value rows in the PV
   // layout; rows are clamped into the cache (positions >= t1 are masked,
-  // pos itself is substituted from LDS). Nontemporal: each row is read by
-  // the four head blocks of its chunk (same XCD) within one launch.
+  // pos itself is substituted from LDS). Nontemporal: with HPB = 1 each row
+  // is read by the four head blocks of its chunk (same XCD) within one launch.
   float4 kr[8], vr[8];
   auto load_k = [&](int p) {
     const int t = min(t0 + 32 * p + 8 * wv + pl, kv_last);
@@ -735,22 +743,38 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
       dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
     }
   };
-  if (wv == 0) norm_rope(hx, nwt, (float*)qs4);
+  if (HPB == 1) {
+    if (wv == 0) norm_rope(hx, nwt, (float*)qs4[0]);
+  } else if (wv < HPB) {
+    if (wv < nq) norm_rope(hx, nwt, (float*)qs4[wv]);
+    else qs4[wv][lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   if (holder && wv == 1) norm_rope(kx, kwt, (float*)ks4);
   if (holder && wv == 2) vs4[lane] = vme;
   __syncthreads();
-  if (holder && h == 0) {
+  if (holder && h0 == 0) {
     a.k_cache[(size_t)pos * kHeadDim + tid] = ((const float*)ks4)[tid];
     a.v_cache[(size_t)pos * kHeadDim + tid] = ((const float*)vs4)[tid];
   }
-  if (b == 0 && a.q_dbg && tid < 64) *(float4*)(a.q_dbg + h * kHeadDim + 4 * tid) = qs4[tid];
-
-  float4 qr[8];
+  if (b == 0 && a.q_dbg && tid < 64)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) qr[j] = qs4[oc + 8 * j];
+    for (int hh = 0; hh < HPB; ++hh)
+      if (h0 + hh < nq) *(float4*)(a.q_dbg + (h0 + hh) * kHeadDim + 4 * tid) = qs4[hh][tid];
 
-  float m = -INFINITY, l = 0.f;
-  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 qr[HPB][8];
+#pragma unroll
+  for (int hh = 0; hh < HPB; ++hh)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[hh][j] = qs4[hh][oc + 8 * j];
+
+  float m[HPB], l[HPB];
+  float4 o4[HPB];
+#pragma unroll
+  for (int hh = 0; hh < HPB; ++hh) {
+    m[hh] = -INFINITY;
+    l[hh] = 0.f;
+    o4[hh] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   for (int p = 0; p < npass; ++p) {
     const int tb = t0 + 32 * p + 8 * wv;       // first position of this wave's pass
     const int t = tb + pl;
@@ -758,77 +782,152 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = ks4[oc + 8 * j];
     }
-    float d = 0.f;
+    float sc[HPB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      d = fmaf(qr[j].x, kr[j].x, d);
-      d = fmaf(qr[j].y, kr[j].y, d);
-      d = fmaf(qr[j].z, kr[j].z, d);
-      d = fmaf(qr[j].w, kr[j].w, d);
+    for (int hh = 0; hh < HPB; ++hh) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d = fmaf(qr[hh][j].x, kr[j].x, d);
+        d = fmaf(qr[hh][j].y, kr[j].y, d);
+        d = fmaf(qr[hh][j].z, kr[j].z, d);
+        d = fmaf(qr[hh][j].w, kr[j].w, d);
+      }
+      d = group8_sum(d);
+      sc[hh] = (t < t1 && h0 + hh < nq) ? d * a.scale : -INFINITY;
     }
-    d = group8_sum(d);
-    const float sc = (t < t1) ? d * a.scale : -INFINITY;
     load_k(p + 1 < npass ? p + 1 : p);          // next pass (a repeat on the last)
-    const float mx = across8_max(sc);
-    const float mn = fmaxf(m, mx);
-    const float alpha = (m == -INFINITY) ? 0.f : expf(m - mn);
-    const float pr = (sc == -INFINITY) ? 0.f : expf(sc - mn);
-    l = fmaf(l, alpha, across8_sum(pr));
-    m = mn;
+    float pr[HPB], alpha[HPB];
+#pragma unroll
+    for (int hh = 0; hh < HPB; ++hh) {
+      const float mx = across8_max(sc[hh]);
+      const float mn = fmaxf(m[hh], mx);
+      alpha[hh] = (m[hh] == -INFINITY) ? 0.f : expf(m[hh] - mn);
+      pr[hh] = (sc[hh] == -INFINITY) ? 0.f : expf(sc[hh] - mn);
+      l[hh] = fmaf(l[hh], alpha[hh], across8_sum(pr[hh]));
+      m[hh] = mn;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (tb + i == pos) vr[i] = vs4[lane];
-    o4.x *= alpha;
-    o4.y *= alpha;
-    o4.z *= alpha;
-    o4.w *= alpha;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), 8 * i));
-      o4.x = fmaf(pv, vr[i].x, o4.x);
-      o4.y = fmaf(pv, vr[i].y, o4.y);
-      o4.z = fmaf(pv, vr[i].z, o4.z);
-      o4.w = fmaf(pv, vr[i].w, o4.w);
+    for (int hh = 0; hh < HPB; ++hh) {
+      o4[hh].x *= alpha[hh];
+      o4[hh].y *= alpha[hh];
+      o4[hh].z *= alpha[hh];
+      o4[hh].w *= alpha[hh];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[hh]), 8 * i));
+        o4[hh].x = fmaf(pv, vr[i].x, o4[hh].x);
+        o4[hh].y = fmaf(pv, vr[i].y, o4[hh].y);
+        o4[hh].z = fmaf(pv, vr[i].z, o4[hh].z);
+        o4[hh].w = fmaf(pv, vr[i].w, o4[hh].w);
+      }
     }
     load_v(p + 1 < npass ? p + 1 : p);
   }
 
-  // merge the four waves (fixed order) into the chunk's (max, sum, o)
-  wo[wv][lane] = o4;
-  if (lane == 0) {
-    wm[wv] = m;
-    wl[wv] = l;
+  // merge the four waves (fixed order) into the chunk's (max, sum, o) per head
+#pragma unroll
+  for (int hh = 0; hh < HPB; ++hh) {
+    wo[wv][hh][lane] = o4[hh];
+    if (lane == 0) {
+      wm[wv][hh] = m[hh];
+      wl[wv][hh] = l[hh];
+    }
   }
   __syncthreads();
-  if (tid == 0) {
-    const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  if (tid < HPB) {
+    const int hh = tid;
+    const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = wm[w] == -INFINITY ? 0.f : expf(wm[w] - M);
-      fw[w] = f;
-      L = fmaf(f, wl[w], L);
+      const float f = wm[w][hh] == -INFINITY ? 0.f : expf(wm[w][hh] - M);
+      fw[w][hh] = f;
+      L = fmaf(f, wl[w][hh], L);
     }
-    hst[0] = M;
-    hst[1] = L;
+    hst[hh][0] = M;
+    hst[hh][1] = L;
   }
   __syncthreads();
   if (tid < 64) {
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float f = fw[w];
-      const float4 v = wo[w][tid];
-      O.x = fmaf(f, v.x, O.x);
-      O.y = fmaf(f, v.y, O.y);
-      O.z = fmaf(f, v.z, O.z);
-      O.w = fmaf(f, v.w, O.w);
+    for (int hh = 0; hh < HPB; ++hh) {
+      const int h = h0 + hh;
+      if (h >= nq) break;
+      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = fw[w][hh];
+        const float4 v = wo[w][hh][tid];
+        O.x = fmaf(f, v.x, O.x);
+        O.y = fmaf(f, v.y, O.y);
+        O.z = fmaf(f, v.z, O.z);
+        O.w = fmaf(f, v.w, O.w);
+      }
+      *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = O;
+      if (tid == 0) {
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[hh][0];
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[hh][1];
+      }
     }
-    *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = O;
-    if (tid == 0) {
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[0];
-      a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Long-span decode attention merge: per query head, the softmax-weighted sum
+// of the launch's nch chunk partials, o = sum_c f_c o_c / sum_c f_c l_c with
+// f_c = exp(m_c - max_c m_c) (empty chunks have m_c = -inf, f_c = 0), written
+// to attn_out, the O GEMV's input. Block (32-dim slice, head); thread (chunk
+// group tid / 32 of 8, dim tid % 32) sums chunks g, g + 8, ..., then the
+// groups add in a fixed order (deterministic).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a, int nch) {
+  constexpr int kPer = kDecMaxChunks / 8;   // chunks per thread
+  __shared__ float gmax[8], gl[8], go[8][32];
+  const int tid = threadIdx.x, cg = tid >> 5, d = tid & 31;
+  const int h = blockIdx.y, dim = 32 * blockIdx.x + d;
+  const float* ml = a.part + kDecStatOff;
+  // every partial of this thread is loaded before any is used (the loads
+  // are independent; one at a time each would wait a full memory latency)
+  float2 st[kPer];
+  float ov[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int c = min(cg + 8 * k, nch - 1);
+    st[k] = *(const float2*)(ml + ((size_t)c * kAttnMaxQ + h) * 2);
+    ov[k] = a.part[((size_t)c * kAttnMaxQ + h) * kHeadDim + dim];
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (cg + 8 * k < nch) mx = fmaxf(mx, st[k].x);
+  if (d == 0) gmax[cg] = mx;
+  __syncthreads();
+  float M = gmax[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) M = fmaxf(M, gmax[i]);
+  float L = 0.f, O = 0.f;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (cg + 8 * k < nch) {
+      const float f = expf(st[k].x - M);
+      L = fmaf(f, st[k].y, L);
+      O = fmaf(f, ov[k], O);
     }
+  go[cg][d] = O;
+  if (d == 0) gl[cg] = L;
+  __syncthreads();
+  if (cg == 0) {
+    float So = 0.f, Sl = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      So += go[i][d];
+      Sl += gl[i];
+    }
+    a.attn_out[h * kHeadDim + dim] = So / Sl;
   }
 }
 
@@ -1748,7 +1847,15 @@ int launch_gemv(int pro, int epi, int ci, const GemvArgs& a, void* stream) {
 
 int launch_attention(const AttnArgs& a, int grid, void* stream) {
   if (a.n_q < 1 || a.n_q > kAttnMaxQ || grid < 1 || grid > kDecMaxChunks) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_dec, dim3(grid, a.n_q), dim3(256), 0, (hipStream_t)stream, a);
+  if (grid <= kDecMergeInO) hipLaunchKernelGGL(k_attn_dec<1>, dim3(grid, a.n_q), dim3(256), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(k_attn_dec<kAttnMaxQ>, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_attention_merge(const AttnArgs& a, int chunks, void* stream) {
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || chunks < 1 || chunks > kDecMaxChunks || !a.part || !a.attn_out)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_merge, dim3(kHeadDim / 32, a.n_q), dim3(256), 0, (hipStream_t)stream, a, chunks);
   return (int)hipGetLastError();
 }
 

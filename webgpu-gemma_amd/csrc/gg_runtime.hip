@@ -256,19 +256,29 @@ int record_forward_impl(gg_ctx* c, bool final_norm) {
     at.part = c->attn_part;
     at.attn_out = c->attn_out;
     at.q_dbg = c->q_dbg + (size_t)l * c->QD;
+    // up to 16 chunks (spans <= 4096): one block per (chunk, head), merged by
+    // the O GEMV's prologue; longer spans: 256 chunks of all four heads, merged
+    // by k_attn_merge into attn_out
+    const int nch = decode_attention_chunks(c->CTX, at.window);
+    const bool merge_in_o = nch <= kDecMergeInO;
     {
       ProbeScope ps(c, GG_PROBE_ATTN, l);
-      GG_TRY(launch_rc(c, launch_attention(at, decode_attention_chunks(c->CTX, at.window), c->stream), "attention"));
+      GG_TRY(launch_rc(c, launch_attention(at, nch, c->stream), "attention"));
+      if (!merge_in_o) GG_TRY(launch_rc(c, launch_attention_merge(at, nch, c->stream), "attention merge"));
     }
-    // O projection; its prologue merges the attention chunks into attn_out
     GemvArgs o = gemv_base(Ly.o, c->lay_o, c->o_out);
-    o.attn_part = c->attn_part;
-    o.attn_chunks = decode_attention_chunks(c->CTX, at.window);
-    o.x_out = c->attn_out;
-    o.st = c->st;
+    if (merge_in_o) {
+      o.attn_part = c->attn_part;
+      o.attn_chunks = nch;
+      o.x_out = c->attn_out;
+      o.st = c->st;
+    } else {
+      o.x = c->attn_out;
+    }
     {
       ProbeScope ps(c, GG_PROBE_O, l);
-      GG_TRY(launch_rc(c, launch_gemv(PRO_ATTN_MERGE, EPI_OUT, c->lay_o.CI, o, c->stream), "o gemv"));
+      GG_TRY(launch_rc(c, launch_gemv(merge_in_o ? PRO_ATTN_MERGE : PRO_NONE, EPI_OUT, c->lay_o.CI, o, c->stream),
+                       "o gemv"));
     }
     // gate/up with post-attn norm + residual + ffn_norm, GeGLU epilogue
     GemvArgs gu = gemv_base(Ly.gu, c->lay_gu, nullptr);
