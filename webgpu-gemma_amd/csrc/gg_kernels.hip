@@ -1223,16 +1223,18 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   };
   // V^T as bf16 hi / lo planes, 32 keys (64 bytes) per dim row; the 16-byte
   // unit u (keys 8u .. 8u + 7) of dim row d sits at u ^ ((d / 2) % 4). Wave h
-  // fetches keys 8 h .. 8 h + 7, lane l dims l + 64 e, and writes unit h of
-  // its four dim rows.
+  // fetches keys 8 h .. 8 h + 7, lane l dims 4 l .. 4 l + 3 (one 16-byte load
+  // per key), and writes unit h of its four dim rows.
   float vv[8][4];
   auto fetch_v = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int key = kt + 8 * h + i;
-      const float* vr = a.v_cache + (size_t)(key < k1 ? key : k0) * kHeadDim + lane;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vv[i][e] = key < k1 ? vr[64 * e] : 0.f;
+      const float4 x = *(const float4*)(a.v_cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
+      vv[i][0] = key < k1 ? x.x : 0.f;
+      vv[i][1] = key < k1 ? x.y : 0.f;
+      vv[i][2] = key < k1 ? x.z : 0.f;
+      vv[i][3] = key < k1 ? x.w : 0.f;
     }
   };
   auto stage_v = [&]() {
@@ -1244,7 +1246,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
         hi[i] = (__bf16)vv[i][e];
         lo[i] = (__bf16)(vv[i][e] - (float)hi[i]);
       }
-      const int d = lane + 64 * e;
+      const int d = 4 * lane + e;
       const int o = d * kPfKeys + 8 * (h ^ ((d >> 1) & 3));
       *(bf16x8*)&Vh[o] = hi;
       *(bf16x8*)&Vl[o] = lo;
@@ -1256,6 +1258,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   const int row = qt * kPfRows + c16;
   const bool row_ok = row < M;
   const int prow = a.pf_start + row, plo = pf_key_lo(a, prow);
+  const float sl2 = a.scale * 1.4426950408889634f;   // scores in log2 units (softmax in base 2)
+  // keys [kt, kt + 31] are valid for every row of the tile: all rows exist,
+  // the last key is <= the first row's position and < k1, and the first key
+  // is >= the last row's window start
+  const int r_first = a.pf_start + qt * kPfRows, r_last = r_first + kPfRows - 1;
+  const bool rows_full = qt * kPfRows + kPfRows <= M;
+  const int lo_last = pf_key_lo(a, r_last);
+  auto tile_full = [&](int kt) { return rows_full && kt + kPfKeys - 1 <= r_first && kt + kPfKeys <= k1 && kt >= lo_last; };
   const float* qp = a.qkv + (size_t)min(row, M - 1) * (nq * kHeadDim + 2 * kHeadDim) + min(h, nq - 1) * kHeadDim + 8 * g;
   bf16x8 qh[8], ql[8];
 #pragma unroll
@@ -1297,28 +1307,39 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
           s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[t], s[j], 0, 0, 0);
         }
       }
-      // scale + causal / window mask; online softmax of row l % 16
+      // scale (to log2 units) + causal / window mask; online softmax of row
+      // l % 16 in base 2. A tile inside every row's key range needs no mask.
       float mx = -INFINITY;
+      if (tile_full(kt)) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kt + 8 * g + 4 * j + r;
-          const bool ok = row_ok && key < k1 && key >= plo && key <= prow;
-          p[j][r] = ok ? s[j][r] * a.scale : -INFINITY;
-          mx = fmaxf(mx, p[j][r]);
-        }
+          for (int r = 0; r < 4; ++r) {
+            p[j][r] = s[j][r] * sl2;
+            mx = fmaxf(mx, p[j][r]);
+          }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kt + 8 * g + 4 * j + r;
+            const bool ok = row_ok && key < k1 && key >= plo && key <= prow;
+            p[j][r] = ok ? s[j][r] * sl2 : -INFINITY;
+            mx = fmaxf(mx, p[j][r]);
+          }
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mn = fmaxf(m, mx);
       const float mb = mn == -INFINITY ? 0.f : mn;   // a row with no key yet keeps p = 0
-      alpha = expf(m - mb);
+      alpha = __builtin_amdgcn_exp2f(m - mb);
       float ps = 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[j][r] = expf(p[j][r] - mb);
+          p[j][r] = __builtin_amdgcn_exp2f(p[j][r] - mb);
           ps += p[j][r];
         }
       l = fmaf(l, alpha, ps);
@@ -1330,13 +1351,16 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
     __syncthreads();   // V of this tile staged
     if (active) {
       // O rows 4 g + r take the factors of the lanes that hold those rows
-      float ar[4];
+      // (skipped when no row's running max moved: every factor is then 1)
+      if (__ballot(alpha != 1.f)) {
+        float ar[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
+        for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < 16; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[i][r] *= ar[r];
+          for (int r = 0; r < 4; ++r) o[i][r] *= ar[r];
+      }
       // O += P V on bf16 MFMA: A = P (row l % 16, keys 8 g .. 8 g + 7 =
       // p[j][r] for key 8 g + 4 j + r), B = V^T rows; hi.hi, lo.hi, hi.lo
       bf16x8 ph, pl;
@@ -1390,7 +1414,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
 }
 
 // Rows of query tiles with more than one chunk: softmax-weighted sum of the
-// chunks' (m, l, O), one block per row, thread = head dim.
+// chunks' (m, l, O) (maxima in log2 units, as k_attn_pf keeps them), one
+// block per row, thread = head dim.
 __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
   const int row = blockIdx.x, tid = threadIdx.x, nq = a.n_q;
   int klo, khi, nkc;
@@ -1403,7 +1428,7 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
     float L = 0.f, O = 0.f;
     for (int c = 0; c < nkc; ++c) {
       const float* pc = pr + (c * nq + h) * (2 + kHeadDim);
-      const float f = pc[0] == -INFINITY ? 0.f : expf(pc[0] - M);
+      const float f = pc[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pc[0] - M);
       L = fmaf(f, pc[1], L);
       O = fmaf(f, pc[2 + tid], O);
     }
