@@ -7,7 +7,9 @@
 //   k_attn_dec      QK-norm + RoPE + KV store + one chunk of decode attention
 //                   per block, chunk partials to memory (engine.ts:775-783)
 //   k_gemv_mg<ATTN_MERGE, OUT>  merges the attention chunks in its prologue,
-//                   then the attention output projection (engine.ts:784)
+//                   then the attention output projection (engine.ts:784);
+//                   spans above 4096 positions: k_attn_merge, then
+//                   k_gemv_mg<NONE, OUT>
 //   k_gemv_mg<RESID_NORM, GEGLU>  post-attn norm + residual + ffn_norm, gate
 //                   and up rows side by side, GeGLU in the epilogue (engine.ts:785-792)
 //   k_gemv_mg<NONE, OUT>       down projection (engine.ts:793)
@@ -18,7 +20,8 @@
 // A batched prefill runs per layer the bf16-MFMA GEMMs (k_gemm: int8 weights
 // exact in bf16, activations split into bf16 hi + lo), the row kernels
 // (norms, residuals, QK-norm + RoPE + KV store) and the MFMA attention
-// k_attn_pf (+ k_attn_pf_merge for long spans).
+// k_attn_pf (+ k_attn_pf_merge for long spans); the GEMM tiles are 128 x 128,
+// or 128 x 144 for 1152-wide outputs with a K split.
 //
 // On this multi-XCD part a device-scope fence is a whole-L2 write-back, so
 // kernels never fence and never exchange data across blocks of one launch:
