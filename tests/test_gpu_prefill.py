@@ -100,3 +100,38 @@ def test_1b_batched_prefill_2048_matches_token_by_token(gpu, mode):
         pos += 1
     a.close()
     b.close()
+
+
+def test_1b_batched_prefill_ragged_slices_long_span(gpu):
+    """Gemma-3-1B shapes at contextLength 8192, gemma3 attention: a 6000-id
+    prompt prefilled in ragged batched slices (2500 + 2500 + 1000 rows: no
+    slice length or start is a multiple of the 128-row GEMM tile, and the
+    global layers' key spans reach 6000) against the token-by-token path;
+    then decode steps past 4096 positions (256-chunk attention + merge)."""
+    shape = synth.GEMMA3_1B.with_ctx(8192).gemma3_mode()
+    say("1b ragged batched prefill, 6000 ids")
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    prompt = synth.prompt_ids(6000, seed=6000, vocab=shape.vocab)
+    a = engine(shape, t, 2500)
+    a.prefill(prompt, 0)
+    b = engine(shape, t, 0)
+    b.prefill(prompt, 0)
+    say("1b prefilled both")
+    for l in range(shape.layers):
+        assert rel(a.read(capi.READ_LAYER_HIDDEN, l), b.read(capi.READ_LAYER_HIDDEN, l)) < TOL, l
+    for l in (0, 5, 11, 25):
+        ka = a.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:6000]
+        kb = b.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:6000]
+        assert rel(ka, kb) < TOL, l
+    ta, tb = a.select(), b.select()
+    assert rel(a.read(capi.READ_LOGITS), b.read(capi.READ_LOGITS)) < TOL
+    assert ta == tb
+    pos = 6000
+    for _ in range(6):
+        ta, tb = a.step(ta, pos), b.step(tb, pos)
+        assert ta == tb
+        pos += 1
+    a.close()
+    b.close()
