@@ -237,11 +237,11 @@ int launch_rows_resid(const RowArgs& a, void* stream);
 int launch_rows_kv(const RowArgs& a, void* stream);
 constexpr int kGemmMaxSlices = 4;   // K slices of a prefill GEMM (summed by the consumer)
 constexpr int kPrefillChunks = 16;   // key chunks per query tile in the batched prefill attention
-constexpr int kPrefillMinChunk = 256;
-// Longest key span of a 16-row query tile of a prefill of M rows at `start`.
+constexpr int kPrefillMinChunk = 160;
+// Longest key span of a 32-row query tile of a prefill of M rows at `start`.
 inline int prefill_max_span(int window, int start, int M) {
   const int full = start + M;
-  return window > 0 && window + 15 < full ? window + 15 : full;
+  return window > 0 && window + 31 < full ? window + 31 : full;
 }
 // Keys per chunk: a multiple of 32, >= kPrefillMinChunk, at most kPrefillChunks chunks.
 inline int prefill_chunk(int window, int start, int M) {

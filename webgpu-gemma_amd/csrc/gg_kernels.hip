@@ -1127,9 +1127,11 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
 // one prompt token per decode pass, engine.ts:923-928, with the
 // scores / softmax / weighted V of shaders.ts:229-325).
 //
-// Block (x = key chunk, y = query tile) covers 16 prompt rows; wave h
-// computes query head h of those rows over the chunk's keys, which are
-// staged 32 rows at a time in LDS and shared by the heads (one KV head).
+// Block (x = key chunk, y = query tile) covers 32 prompt rows with 8 waves;
+// wave w computes query head w % 4 of rows 16 (w / 4) .. + 15 over the
+// chunk's keys, which are staged 32 rows at a time in LDS and shared by the
+// heads (one KV head) and both row halves, so each key's hi / lo split
+// serves 128 (row, head) pairs.
 //   S^T = K Q^T  on v_mfma_f32_16x16x32_bf16 with q and k split into bf16
 //                hi + lo (k and v when they are staged, q once per block):
 //                per 32 dims the products hi.hi, lo.hi and hi.lo, fp32
@@ -1159,7 +1161,7 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t* hi, uint16_t* lo) 
   *lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
 
-constexpr int kPfRows = 16;   // query rows per block (one MFMA tile)
+constexpr int kPfRows = 32;   // query rows per block: two 16-row MFMA tiles
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
@@ -1172,7 +1174,8 @@ __device__ __forceinline__ int pf_key_lo(const AttnArgs& a, int pos) {
   return a.window > 0 ? max(0, pos - a.window + 1) : 0;
 }
 
-// Keys of query tile qt: [lo(first row), last row], chunks of pf_chunk keys.
+// Keys of query tile qt (kPfRows rows): [lo(first row), last row], chunks of
+// pf_chunk keys.
 __device__ __forceinline__ void pf_tile_span(const AttnArgs& a, int qt, int* klo, int* khi, int* nkc) {
   const int p_first = a.pf_start + qt * kPfRows;
   const int p_last = a.pf_start + min(qt * kPfRows + kPfRows - 1, a.pf_rows - 1);
@@ -1181,12 +1184,12 @@ __device__ __forceinline__ void pf_tile_span(const AttnArgs& a, int qt, int* klo
   *nkc = (p_last - *klo + a.pf_chunk) / a.pf_chunk;
 }
 
-__global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
+__global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   __shared__ __align__(16) uint16_t Kh[kPfKeys * kHeadDim];
   __shared__ __align__(16) uint16_t Kl[kPfKeys * kHeadDim];
   __shared__ __align__(16) uint16_t Vh[kHeadDim * kPfKeys];   // V^T: [dim][key]
   __shared__ __align__(16) uint16_t Vl[kHeadDim * kPfKeys];
-  const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w8 = tid >> 6, h = w8 & 3, rt = w8 >> 2;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.pf_rows, nq = a.n_q, qt = blockIdx.y, kc = blockIdx.x;
   int klo, khi, nkc;
@@ -1195,14 +1198,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   const int k0 = klo + kc * a.pf_chunk, k1 = min(k0 + a.pf_chunk, khi + 1);
   const bool active = h < nq;
 
-  // K staging: wave w moves key rows 4 i + w of a tile, lane = float4 slot.
+  // K staging: wave w moves key rows 8 i + w of a tile, lane = float4 slot.
   // V of a tile is fetched while its scores run, K of the next tile while
   // the weighted sum runs, so the two staging sets are never live together.
-  float4 st[8];
+  float4 st[4];
   auto fetch = [&](const float* cache, int kt) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = kt + 4 * i + h;
+    for (int i = 0; i < 4; ++i) {
+      const int key = kt + 8 * i + w8;
       st[i] = *(const float4*)(cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
       if (key >= k1) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -1213,8 +1216,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   auto kswz = [](int kr) { return (kr & 3) | ((kr >> 3) << 2); };
   auto stage_k = [&]() {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int kr = 4 * i + h;
+    for (int i = 0; i < 4; ++i) {
+      const int kr = 8 * i + w8;
       const float4 x = st[i];
       const bf16x4 hi = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
       const bf16x4 lo = {(__bf16)(x.x - (float)hi[0]), (__bf16)(x.y - (float)hi[1]), (__bf16)(x.z - (float)hi[2]),
@@ -1225,14 +1228,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
     }
   };
   // V^T as bf16 hi / lo planes, 32 keys (64 bytes) per dim row; the 16-byte
-  // unit u (keys 8u .. 8u + 7) of dim row d sits at u ^ ((d / 2) % 4). Wave h
-  // fetches keys 8 h .. 8 h + 7, lane l dims 4 l .. 4 l + 3 (one 16-byte load
-  // per key), and writes unit h of its four dim rows.
-  float vv[8][4];
+  // unit u (keys 8u .. 8u + 7) of dim row d sits at u ^ ((d / 2) % 4). Wave w
+  // fetches keys 4 w .. 4 w + 3, lane l dims 4 l .. 4 l + 3 (one 16-byte load
+  // per key), and writes half w % 2 of unit w / 2 of its four dim rows.
+  float vv[4][4];
   auto fetch_v = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = kt + 8 * h + i;
+    for (int i = 0; i < 4; ++i) {
+      const int key = kt + 4 * w8 + i;
       const float4 x = *(const float4*)(a.v_cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
       vv[i][0] = key < k1 ? x.x : 0.f;
       vv[i][1] = key < k1 ? x.y : 0.f;
@@ -1243,30 +1246,30 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   auto stage_v = [&]() {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      bf16x8 hi, lo;
+      bf16x4 hi, lo;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 4; ++i) {
         hi[i] = (__bf16)vv[i][e];
         lo[i] = (__bf16)(vv[i][e] - (float)hi[i]);
       }
       const int d = 4 * lane + e;
-      const int o = d * kPfKeys + 8 * (h ^ ((d >> 1) & 3));
-      *(bf16x8*)&Vh[o] = hi;
-      *(bf16x8*)&Vl[o] = lo;
+      const int o = d * kPfKeys + 8 * ((w8 >> 1) ^ ((d >> 1) & 3)) + 4 * (w8 & 1);
+      *(bf16x4*)&Vh[o] = hi;
+      *(bf16x4*)&Vl[o] = lo;
     }
   };
   fetch(a.k_cache, k0);
 
   // q (normed + roped) of row l % 16, dims 32 t + 8 g .. +7, as bf16 hi / lo
-  const int row = qt * kPfRows + c16;
+  const int row = qt * kPfRows + rt * 16 + c16;
   const bool row_ok = row < M;
   const int prow = a.pf_start + row, plo = pf_key_lo(a, prow);
   const float sl2 = a.scale * 1.4426950408889634f;   // scores in log2 units (softmax in base 2)
   // keys [kt, kt + 31] are valid for every row of the tile: all rows exist,
   // the last key is <= the first row's position and < k1, and the first key
   // is >= the last row's window start
-  const int r_first = a.pf_start + qt * kPfRows, r_last = r_first + kPfRows - 1;
-  const bool rows_full = qt * kPfRows + kPfRows <= M;
+  const int r_first = a.pf_start + qt * kPfRows + rt * 16, r_last = r_first + 15;
+  const bool rows_full = qt * kPfRows + rt * 16 + 16 <= M;
   const int lo_last = pf_key_lo(a, r_last);
   auto tile_full = [&](int kt) { return rows_full && kt + kPfKeys - 1 <= r_first && kt + kPfKeys <= k1 && kt >= lo_last; };
   const float* qp = a.qkv + (size_t)min(row, M - 1) * (nq * kHeadDim + 2 * kHeadDim) + min(h, nq - 1) * kHeadDim + 8 * g;
@@ -1397,7 +1400,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int orow = qt * kPfRows + 4 * g + r;
+    const int orow = qt * kPfRows + rt * 16 + 4 * g + r;
     if (orow >= M) continue;
     if (nkc == 1) {
       uint16_t* out = a.pf_out + (size_t)orow * nq * kHeadDim + h * kHeadDim + c16;
@@ -1418,26 +1421,24 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(AttnArgs a) {
 
 // Rows of query tiles with more than one chunk: softmax-weighted sum of the
 // chunks' (m, l, O) (maxima in log2 units, as k_attn_pf keeps them), one
-// block per row, thread = head dim.
+// block per (row, query head), thread = head dim.
 __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
-  const int row = blockIdx.x, tid = threadIdx.x, nq = a.n_q;
+  const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nq = a.n_q;
   int klo, khi, nkc;
   pf_tile_span(a, row / kPfRows, &klo, &khi, &nkc);
   if (nkc == 1) return;
   const float* pr = a.part + (size_t)row * kPrefillChunks * nq * (2 + kHeadDim);
-  for (int h = 0; h < nq; ++h) {
-    float M = -INFINITY;
-    for (int c = 0; c < nkc; ++c) M = fmaxf(M, pr[(c * nq + h) * (2 + kHeadDim)]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < nkc; ++c) {
-      const float* pc = pr + (c * nq + h) * (2 + kHeadDim);
-      const float f = pc[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pc[0] - M);
-      L = fmaf(f, pc[1], L);
-      O = fmaf(f, pc[2 + tid], O);
-    }
-    const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + tid;
-    split_bf16(O / L, &a.pf_out[e], &a.pf_out[(size_t)a.pf_rows * nq * kHeadDim + e]);
+  float M = -INFINITY;
+  for (int c = 0; c < nkc; ++c) M = fmaxf(M, pr[(c * nq + h) * (2 + kHeadDim)]);
+  float L = 0.f, O = 0.f;
+  for (int c = 0; c < nkc; ++c) {
+    const float* pc = pr + (c * nq + h) * (2 + kHeadDim);
+    const float f = pc[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pc[0] - M);
+    L = fmaf(f, pc[1], L);
+    O = fmaf(f, pc[2 + tid], O);
   }
+  const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + tid;
+  split_bf16(O / L, &a.pf_out[e], &a.pf_out[(size_t)a.pf_rows * nq * kHeadDim + e]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1894,8 +1895,8 @@ int launch_prefill_attention(const AttnArgs& a, int M, void* stream) {
   const int span = prefill_max_span(a.window, a.pf_start, M);
   const int nkc = (span + a.pf_chunk - 1) / a.pf_chunk;
   if (nkc > kPrefillChunks) return (int)hipErrorInvalidValue;   // `part` holds kPrefillChunks per row
-  hipLaunchKernelGGL(k_attn_pf, dim3(nkc, (M + kPfRows - 1) / kPfRows), dim3(256), 0, (hipStream_t)stream, a);
-  if (nkc > 1) hipLaunchKernelGGL(k_attn_pf_merge, dim3(M), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_attn_pf, dim3(nkc, (M + kPfRows - 1) / kPfRows), dim3(512), 0, (hipStream_t)stream, a);
+  if (nkc > 1) hipLaunchKernelGGL(k_attn_pf_merge, dim3(M, a.n_q), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
