@@ -213,8 +213,9 @@ def main():
                     help="fill the context token by token (the reference's prefillBatched) instead of batched")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the token loop at batch 1 "
-              f"runs on a single MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the batch-1 token loop runs on "
+              f"a single MI355X, and more GPUs serve more independent conversations (one context per GPU, no "
+              f"exchange) rather than one faster one", file=sys.stderr)
         sys.exit(2)
 
     if args.copy_calibration:

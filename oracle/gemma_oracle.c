@@ -1,7 +1,8 @@
 /*
  * gemma_oracle.c -- CPU restatement of the webgpu-gemma token loop.
  *
- * TEST INFRASTRUCTURE ONLY (the checker for the HIP path; see the header).
+ * TEST INFRASTRUCTURE ONLY (the oracle the HIP path is tested against; see
+ * the header).
  * Built with -O2 -ffp-contract=off -fopenmp so that every fp32 expression
  * rounds exactly as written, in the order the WGSL source writes it.
  * OpenMP only splits independent output rows; each row's sum keeps the

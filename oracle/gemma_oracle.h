@@ -1,7 +1,7 @@
 /*
  * gemma_oracle.h -- CPU restatement of the webgpu-gemma token loop.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP path:
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle the HIP path is tested against:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it. Nothing in the product (libgg.so, the JS host) links or calls it.
  *

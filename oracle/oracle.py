@@ -1,6 +1,6 @@
 """ctypes wrapper of the C oracle (libgemma_oracle.so).
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP path. Only tests/,
+TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against. Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
 """
 from __future__ import annotations
