@@ -135,3 +135,33 @@ def test_1b_batched_prefill_ragged_slices_long_span(gpu):
         pos += 1
     a.close()
     b.close()
+
+
+def test_270m_batched_prefill_matches_oracle(gpu):
+    """Gemma-3-270M architecture (hidden 640: 128-wide GEMM tiles with a K
+    split, 64-row prompt), gemma3 attention: the 64-id prompt in one batched
+    prefill against the oracle's token-by-token prefill (per-layer hidden,
+    K/V cache, normed hidden), then 32 greedy tokens identical to it."""
+    shape = synth.GEMMA3_270M.gemma3_mode()
+    say("270m batched prefill")
+    t = synth.make_model(shape, seed=270)
+    e = engine(shape, t, 64)
+    o = orc.OracleModel(shape, t)
+    prompt = synth.prompt_ids(64, seed=64, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    for l in range(shape.layers):
+        assert rel(e.read(capi.READ_LAYER_HIDDEN, l), o.buffer(orc.GOR_LAYER_HIDDEN, l)) < TOL, l
+    for l in (0, 5, 17):
+        kc = e.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:64]
+        assert rel(kc, o.buffer(orc.GOR_K_CACHE, l).reshape(shape.ctx, 256)[:64]) < TOL, l
+    assert rel(e.read(capi.READ_NORMED), o.buffer(orc.GOR_NORMED)) < TOL
+    tok = e.select()
+    assert tok == o.select()
+    pos = 64
+    for step in range(32):
+        nxt = e.step(tok, pos)
+        o.forward(tok, pos)
+        assert nxt == o.select(), f"step {step}"
+        tok, pos = nxt, pos + 1
+    e.close()
