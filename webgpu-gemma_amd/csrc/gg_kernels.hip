@@ -1194,7 +1194,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   __shared__ __align__(16) uint16_t Kl[kPfKeys * kHeadDim];
   __shared__ __align__(16) uint16_t Vh[kHeadDim * kPfKeys];   // V^T: [dim][key]
   __shared__ __align__(16) uint16_t Vl[kHeadDim * kPfKeys];
-  const int tid = threadIdx.x, lane = tid & 63, w8 = tid >> 6, h = w8 & 3, rt = w8 >> 2;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = wv & 3, rt = wv >> 2;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.pf_rows, nq = a.n_q, qt = blockIdx.y, kc = blockIdx.x;
   int klo, khi, nkc;
@@ -1210,7 +1210,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   auto fetch = [&](const float* cache, int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = kt + 8 * i + w8;
+      const int key = kt + 8 * i + wv;
       st[i] = *(const float4*)(cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
       if (key >= k1) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -1222,7 +1222,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   auto stage_k = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int kr = 8 * i + w8;
+      const int kr = 8 * i + wv;
       const float4 x = st[i];
       const bf16x4 hi = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
       const bf16x4 lo = {(__bf16)(x.x - (float)hi[0]), (__bf16)(x.y - (float)hi[1]), (__bf16)(x.z - (float)hi[2]),
@@ -1240,7 +1240,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   auto fetch_v = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = kt + 4 * w8 + i;
+      const int key = kt + 4 * wv + i;
       const float4 x = *(const float4*)(a.v_cache + (size_t)(key < k1 ? key : k0) * kHeadDim + 4 * lane);
       vv[i][0] = key < k1 ? x.x : 0.f;
       vv[i][1] = key < k1 ? x.y : 0.f;
@@ -1258,7 +1258,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
         lo[i] = (__bf16)(vv[i][e] - (float)hi[i]);
       }
       const int d = 4 * lane + e;
-      const int o = d * kPfKeys + 8 * ((w8 >> 1) ^ ((d >> 1) & 3)) + 4 * (w8 & 1);
+      const int o = d * kPfKeys + 8 * ((wv >> 1) ^ ((d >> 1) & 3)) + 4 * (wv & 1);
       *(bf16x4*)&Vh[o] = hi;
       *(bf16x4*)&Vl[o] = lo;
     }
