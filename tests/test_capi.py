@@ -41,3 +41,15 @@ def test_create_rejects_bad_config_without_touching_a_device():
     lib = capi.lib()
     assert not lib.gg_create(ctypes.byref(cfg))
     assert b"head_dim" in lib.gg_last_error(None)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says
+    why, before anything touches a device."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
