@@ -486,7 +486,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     for (int i = 0; i < EPT; ++i)
       if (has(i)) *(float4*)&xs[xs_index(4 * (tid + NT * i))] = v[i];
   } else if (PRO == PRO_ATTN_MERGE) {
-    // chunk weights exp(m_c - M) with M the running max, in chunk order
+    // chunk weights 2^(m_c - M) (maxima in log2 units) with M the running
+    // max, in chunk order
     float M = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kMB; ++k)
@@ -494,7 +495,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     float L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     auto add = [&](int k, float Mx) {
-      const float f = expf(am_m[k] - Mx);
+      const float f = __builtin_amdgcn_exp2f(am_m[k] - Mx);
       L = fmaf(f, am_l[k], L);
       acc.x = fmaf(f, am_o[k].x, acc.x);
       acc.y = fmaf(f, am_o[k].y, acc.y);
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
 #pragma unroll
       for (int k = 0; k < kMB; ++k)
         if (c0 + k < nch) Mb = fmaxf(Mb, am_m[k]);
-      const float sc = expf(M - Mb);
+      const float sc = __builtin_amdgcn_exp2f(M - Mb);
       L *= sc;
       acc.x *= sc;
       acc.y *= sc;
@@ -775,6 +776,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) qr[hh][j] = qs4[hh][oc + 8 * j];
 
+  // scores in log2 units: the online softmax and every merge of its
+  // partials (chunk maxima in the same units) run in base 2 on v_exp_f32
+  const float sl2 = a.scale * 1.4426950408889634f;
   float m[HPB], l[HPB];
   float4 o4[HPB];
 #pragma unroll
@@ -802,7 +806,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
         d = fmaf(qr[hh][j].w, kr[j].w, d);
       }
       d = group8_sum(d);
-      sc[hh] = (t < t1 && h0 + hh < nq) ? d * a.scale : -INFINITY;
+      sc[hh] = (t < t1 && h0 + hh < nq) ? d * sl2 : -INFINITY;
     }
     load_k(p + 1 < npass ? p + 1 : p);          // next pass (a repeat on the last)
     float pr[HPB], alpha[HPB];
@@ -810,8 +814,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
     for (int hh = 0; hh < HPB; ++hh) {
       const float mx = across8_max(sc[hh]);
       const float mn = fmaxf(m[hh], mx);
-      alpha[hh] = (m[hh] == -INFINITY) ? 0.f : expf(m[hh] - mn);
-      pr[hh] = (sc[hh] == -INFINITY) ? 0.f : expf(sc[hh] - mn);
+      alpha[hh] = (m[hh] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[hh] - mn);
+      pr[hh] = (sc[hh] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[hh] - mn);
       l[hh] = fmaf(l[hh], alpha[hh], across8_sum(pr[hh]));
       m[hh] = mn;
     }
@@ -852,7 +856,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = wm[w][hh] == -INFINITY ? 0.f : expf(wm[w][hh] - M);
+      const float f = wm[w][hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][hh] - M);
       fw[w][hh] = f;
       L = fmaf(f, wl[w][hh], L);
     }
@@ -887,7 +891,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Long-span decode attention merge: per query head, the softmax-weighted sum
 // of the launch's nch chunk partials, o = sum_c f_c o_c / sum_c f_c l_c with
-// f_c = exp(m_c - max_c m_c) (empty chunks have m_c = -inf, f_c = 0), written
+// f_c = 2^(m_c - max_c m_c) (maxima in log2 units; empty chunks have m_c =
+// -inf, f_c = 0), written
 // to attn_out, the O GEMV's input. Block (32-dim slice, head); thread (chunk
 // group tid / 32 of 8, dim tid % 32) sums chunks g, g + 8, ..., then the
 // groups add in a fixed order (deterministic).
@@ -921,7 +926,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs a, int nch) {
 #pragma unroll
   for (int k = 0; k < kPer; ++k)
     if (cg + 8 * k < nch) {
-      const float f = expf(st[k].x - M);
+      const float f = __builtin_amdgcn_exp2f(st[k].x - M);
       L = fmaf(f, st[k].y, L);
       O = fmaf(f, ov[k], O);
     }
