@@ -266,10 +266,11 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
     for (int i = 0; i < kMaxEPT / 4; ++i)
       if (i < n) s1 = fmaf(v[i], v[i], s1);
     const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)K + a.eps);
+    const float ri1 = 1.f / rms1;
 #pragma unroll
     for (int i = 0; i < kMaxEPT / 4; ++i)
       if (i < n) {
-        const float t = (v[i] * wq[i]) / rms1;   // fusedNormAdd, shaders.ts:415
+        const float t = (v[i] * wq[i]) * ri1;   // fusedNormAdd, shaders.ts:415
         r[i] = res[i] + t;
         ss = fmaf(r[i], r[i], ss);
         if (blockIdx.x == 0) {
@@ -279,10 +280,11 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
       }
   }
   const float rms = sqrtf(block_sum256(ss, sh4) / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
+  const float ri = 1.f / rms;
 #pragma unroll
   for (int i = 0; i < kMaxEPT / 4; ++i)
     if (i < n) {
-      const float x = (r[i] * wp[i]) / rms;
+      const float x = (r[i] * wp[i]) * ri;
       xs[xs_index(tid + 256 * i)] = x;
       if (PRO == PRO_RESID_NORM && blockIdx.x == 0 && a.x_out) a.x_out[tid + 256 * i] = x;
     }
@@ -550,11 +552,11 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       float t1 = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) t1 += shw[0][w];
-      const float rms1 = sqrtf(t1 / (float)K + a.eps);
+      const float ri1 = 1.f / sqrtf(t1 / (float)K + a.eps);
 #pragma unroll
       for (int i = 0; i < EPT; ++i)
-        r[i] = make_float4(res[i].x + (v[i].x * wq[i].x) / rms1, res[i].y + (v[i].y * wq[i].y) / rms1,
-                           res[i].z + (v[i].z * wq[i].z) / rms1, res[i].w + (v[i].w * wq[i].w) / rms1);
+        r[i] = make_float4(res[i].x + (v[i].x * wq[i].x) * ri1, res[i].y + (v[i].y * wq[i].y) * ri1,
+                           res[i].z + (v[i].z * wq[i].z) * ri1, res[i].w + (v[i].w * wq[i].w) * ri1);
     }
     float ss = 0.f;
 #pragma unroll
@@ -574,13 +576,13 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     float t2 = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) t2 += shw[1][w];
-    const float rms = sqrtf(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
+    const float ri = 1.f / sqrtf(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
       if (has(i))
         *(float4*)&xs[xs_index(4 * (tid + NT * i))] =
-            make_float4((r[i].x * wp[i].x) / rms, (r[i].y * wp[i].y) / rms, (r[i].z * wp[i].z) / rms,
-                        (r[i].w * wp[i].w) / rms);
+            make_float4((r[i].x * wp[i].x) * ri, (r[i].y * wp[i].y) * ri, (r[i].z * wp[i].z) * ri,
+                        (r[i].w * wp[i].w) * ri);
   }
   __syncthreads();
 
@@ -742,9 +744,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
     ss = wave_sum_dpp(ss);
-    const float rms = sqrtf(ss / (float)kHeadDim + a.eps);
+    const float ri = 1.f / sqrtf(ss / (float)kHeadDim + a.eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) / rms;
+    for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) * ri;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const float x0 = x[j], x1 = x[j + 2];
@@ -967,21 +969,21 @@ __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) s1 = fmaf(v[i], v[i], s1);
-  const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
+  const float ri1 = 1.f / sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
   float s2 = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
-      const float r = res[i] + (v[i] * wq[i]) / rms1;
+      const float r = res[i] + (v[i] * wq[i]) * ri1;
       v[i] = r;
       a.hidden[tid + 256 * i] = r;
       if (a.hist_out) a.hist_out[tid + 256 * i] = r;
       s2 = fmaf(r, r, s2);
     }
-  const float rms2 = sqrtf(block_sum256(s2, sh4) / (float)H + a.eps);
+  const float ri2 = 1.f / sqrtf(block_sum256(s2, sh4) / (float)H + a.eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    if (i < n) a.normed[tid + 256 * i] = (v[i] * wo[i]) / rms2;
+    if (i < n) a.normed[tid + 256 * i] = (v[i] * wo[i]) * ri2;
   if (tid == 0) {
     a.st->pos += 1;
     a.st->cursor += 1;
