@@ -184,13 +184,16 @@ __device__ __forceinline__ float dot_pair(const Pair& P, const float* __restrict
 }
 
 // shaders.ts:153-170 (tanh GELU, argument clamped to +-15) times up.
+// 0.5 x (1 + tanh(arg)) = x / (1 + e^(-2 arg)), evaluated as
+// x * rcp(1 + 2^(-2 log2(e) arg)) on v_exp_f32 / v_rcp_f32 (a few ulp; the
+// tanh form loses the relative precision of 1 + tanh for negative arg).
 __device__ __forceinline__ float gelu_mul(float x, float up) {
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   float a = 1.0f + (k1 * x) * x;
   float arg = (k0 * x) * a;
   arg = fminf(fmaxf(arg, -15.0f), 15.0f);
-  float g = (0.5f * x) * (1.0f + tanhf(arg));
-  return g * up;
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg * -2.8853900817779268f));
+  return (x * sg) * up;
 }
 
 __device__ __forceinline__ int xs_index(int e) { return (e >> 6) * kXPad + (e & 63); }
