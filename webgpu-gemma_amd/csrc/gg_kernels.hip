@@ -1420,8 +1420,9 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
     if (nkc == 1) {
       uint16_t* out = a.pf_out + (size_t)orow * nq * kHeadDim + h * kHeadDim + c16;
       const size_t plane = (size_t)M * nq * kHeadDim;
+      const float il = 1.f / lr[r];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) split_bf16(o[i][r] / lr[r], &out[16 * i], &out[plane + 16 * i]);
+      for (int i = 0; i < 16; ++i) split_bf16(o[i][r] * il, &out[16 * i], &out[plane + 16 * i]);
     } else {
       float* pp = a.part + (((size_t)orow * kPrefillChunks + kc) * nq + h) * (2 + kHeadDim);
 #pragma unroll
@@ -1616,12 +1617,12 @@ __device__ __forceinline__ void row_norm_out(const float* r, const float* w, int
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) ss = fmaf(r[i], r[i], ss);
-  const float rms = sqrtf(block_sum256(ss, sh4) / (float)H + eps);
+  const float ri = 1.f / sqrtf(block_sum256(ss, sh4) / (float)H + eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
       const int e = threadIdx.x + 256 * i;
-      split_bf16((r[i] * w[e]) / rms, &out[e], &out[plane + e]);
+      split_bf16((r[i] * w[e]) * ri, &out[e], &out[plane + e]);
     }
 }
 
@@ -1672,11 +1673,11 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) s1 = fmaf(v[i], v[i], s1);
-  const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
+  const float ri1 = 1.f / sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
-      v[i] = rs[i] + (v[i] * wq[i]) / rms1;
+      v[i] = rs[i] + (v[i] * wq[i]) * ri1;
       a.res_out[o + tid + 256 * i] = v[i];
       if (a.last_hidden && row == a.M - 1) a.last_hidden[tid + 256 * i] = v[i];
     }
@@ -1697,8 +1698,8 @@ __global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
   const float* rt = a.rope + (size_t)pos * kHeadDim;
   const float cs = rt[tid & 127], sn = rt[128 + (tid & 127)];
   auto norm_rope = [&](float x, float wt) {
-    const float rms = sqrtf(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
-    kk[tid] = (x * wt) / rms;
+    const float ri = 1.f / sqrtf(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
+    kk[tid] = (x * wt) * ri;
     __syncthreads();
     const float out = tid < 128 ? kk[tid] * cs - kk[tid + 128] * sn : kk[tid - 128] * sn + kk[tid] * cs;
     __syncthreads();
