@@ -50,6 +50,9 @@ __device__ __forceinline__ float sbyte(uint32_t w, int b) {
   // compiles to v_cvt_f32_i32_sdwa with a sign-extended byte select
   return (float)(int8_t)(w >> (8 * b));
 }
+// 1 / sqrt(x) on v_rsq_f32 (about 1 ulp): every RMSNorm multiplies by it,
+// where the reference divides by sqrt(mean + eps) (shaders.ts:50-53, 415)
+__device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
 __device__ __forceinline__ float f16_lo(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
 }
@@ -268,8 +271,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
 #pragma unroll
     for (int i = 0; i < kMaxEPT / 4; ++i)
       if (i < n) s1 = fmaf(v[i], v[i], s1);
-    const float rms1 = sqrtf(block_sum256(s1, sh4) / (float)K + a.eps);
-    const float ri1 = 1.f / rms1;
+    const float ri1 = rsq(block_sum256(s1, sh4) / (float)K + a.eps);
 #pragma unroll
     for (int i = 0; i < kMaxEPT / 4; ++i)
       if (i < n) {
@@ -282,8 +284,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, float* xs, int 
         }
       }
   }
-  const float rms = sqrtf(block_sum256(ss, sh4) / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
-  const float ri = 1.f / rms;
+  const float ri = rsq(block_sum256(ss, sh4) / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
 #pragma unroll
   for (int i = 0; i < kMaxEPT / 4; ++i)
     if (i < n) {
@@ -555,7 +556,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
       float t1 = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) t1 += shw[0][w];
-      const float ri1 = 1.f / sqrtf(t1 / (float)K + a.eps);
+      const float ri1 = rsq(t1 / (float)K + a.eps);
 #pragma unroll
       for (int i = 0; i < EPT; ++i)
         r[i] = make_float4(res[i].x + (v[i].x * wq[i].x) * ri1, res[i].y + (v[i].y * wq[i].y) * ri1,
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
     float t2 = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) t2 += shw[1][w];
-    const float ri = 1.f / sqrtf(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
+    const float ri = rsq(t2 / (float)K + a.eps);   // rmsNorm, shaders.ts:50-53
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
       if (has(i))
@@ -747,7 +748,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
     ss = wave_sum_dpp(ss);
-    const float ri = 1.f / sqrtf(ss / (float)kHeadDim + a.eps);
+    const float ri = rsq(ss / (float)kHeadDim + a.eps);
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) * ri;
 #pragma unroll
@@ -972,7 +973,7 @@ __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) s1 = fmaf(v[i], v[i], s1);
-  const float ri1 = 1.f / sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
+  const float ri1 = rsq(block_sum256(s1, sh4) / (float)H + a.eps);
   float s2 = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -983,7 +984,7 @@ __global__ __launch_bounds__(256) void k_final(FinalArgs a) {
       if (a.hist_out) a.hist_out[tid + 256 * i] = r;
       s2 = fmaf(r, r, s2);
     }
-  const float ri2 = 1.f / sqrtf(block_sum256(s2, sh4) / (float)H + a.eps);
+  const float ri2 = rsq(block_sum256(s2, sh4) / (float)H + a.eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) a.normed[tid + 256 * i] = (v[i] * wo[i]) * ri2;
@@ -1617,7 +1618,7 @@ __device__ __forceinline__ void row_norm_out(const float* r, const float* w, int
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) ss = fmaf(r[i], r[i], ss);
-  const float ri = 1.f / sqrtf(block_sum256(ss, sh4) / (float)H + eps);
+  const float ri = rsq(block_sum256(ss, sh4) / (float)H + eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
@@ -1673,7 +1674,7 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) s1 = fmaf(v[i], v[i], s1);
-  const float ri1 = 1.f / sqrtf(block_sum256(s1, sh4) / (float)H + a.eps);
+  const float ri1 = rsq(block_sum256(s1, sh4) / (float)H + a.eps);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     if (i < n) {
@@ -1698,7 +1699,7 @@ __global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
   const float* rt = a.rope + (size_t)pos * kHeadDim;
   const float cs = rt[tid & 127], sn = rt[128 + (tid & 127)];
   auto norm_rope = [&](float x, float wt) {
-    const float ri = 1.f / sqrtf(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
+    const float ri = rsq(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
     kk[tid] = (x * wt) * ri;
     __syncthreads();
     const float out = tid < 128 ? kk[tid] * cs - kk[tid + 128] * sn : kk[tid - 128] * sn + kk[tid] * cs;
