@@ -536,7 +536,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mg(GemvArgs a) {
         if (c0 + k < nch) add(k, M);
     }
     if (4 * tid < K) {
-      const float4 xo = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+      const float iL = 1.f / L;
+      const float4 xo = make_float4(acc.x * iL, acc.y * iL, acc.z * iL, acc.w * iL);
       *(float4*)&xs[xs_index(4 * tid)] = xo;
       if (b == 0) *(float4*)(a.x_out + 4 * tid) = xo;
     }
@@ -814,7 +815,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
       d = group8_sum(d);
       sc[hh] = (t < t1 && h0 + hh < nq) ? d * sl2 : -INFINITY;
     }
-    load_k(p + 1 < npass ? p + 1 : p);          // next pass (a repeat on the last)
+    if (p + 1 < npass) load_k(p + 1);          // next pass (wave-uniform)
     float pr[HPB], alpha[HPB];
 #pragma unroll
     for (int hh = 0; hh < HPB; ++hh) {
@@ -843,7 +844,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
         o4[hh].w = fmaf(pv, vr[i].w, o4[hh].w);
       }
     }
-    load_v(p + 1 < npass ? p + 1 : p);
+    if (p + 1 < npass) load_v(p + 1);
   }
 
   // merge the four waves (fixed order) into the chunk's (max, sum, o) per head
