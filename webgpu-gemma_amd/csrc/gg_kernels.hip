@@ -667,7 +667,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
   __shared__ float4 qs4[HPB][64];
   __shared__ float4 ks4[64], vs4[64];
   __shared__ float4 wo[4][HPB][64];
-  __shared__ float wm[4][HPB], wl[4][HPB], fw[4][HPB], hst[HPB][2];
+  __shared__ float wm[4][HPB], wl[4][HPB];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nq = a.n_q;
@@ -847,7 +847,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
     if (p + 1 < npass) load_v(p + 1);
   }
 
-  // merge the four waves (fixed order) into the chunk's (max, sum, o) per head
+  // merge the four waves (fixed order) into the chunk's (max, sum, o) per
+  // head: one barrier, then every lane of wave 0 forms the weights itself
 #pragma unroll
   for (int hh = 0; hh < HPB; ++hh) {
     wo[wv][hh][lane] = o4[hh];
@@ -857,29 +858,18 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
     }
   }
   __syncthreads();
-  if (tid < HPB) {
-    const int hh = tid;
-    const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float f = wm[w][hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][hh] - M);
-      fw[w][hh] = f;
-      L = fmaf(f, wl[w][hh], L);
-    }
-    hst[hh][0] = M;
-    hst[hh][1] = L;
-  }
-  __syncthreads();
   if (tid < 64) {
 #pragma unroll
     for (int hh = 0; hh < HPB; ++hh) {
       const int h = h0 + hh;
       if (h >= nq) break;
+      const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
+      float L = 0.f;
       float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float f = fw[w][hh];
+        const float f = wm[w][hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w][hh] - M);
+        L = fmaf(f, wl[w][hh], L);
         const float4 v = wo[w][hh][tid];
         O.x = fmaf(f, v.x, O.x);
         O.y = fmaf(f, v.y, O.y);
@@ -888,8 +878,8 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a) {
       }
       *(float4*)(a.part + ((size_t)b * kAttnMaxQ + h) * kHeadDim + 4 * tid) = O;
       if (tid == 0) {
-        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = hst[hh][0];
-        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = hst[hh][1];
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2] = M;
+        a.part[kDecStatOff + ((size_t)b * kAttnMaxQ + h) * 2 + 1] = L;
       }
     }
   }
