@@ -159,6 +159,26 @@ int gg_probe_elapsed(gg_ctx* ctx, float* ms);
  * bracket itself, to subtract from gg_probe_elapsed. */
 int gg_probe_overhead(gg_ctx* ctx, float* ms);
 
+/* Decode path of the per-token forward passes. GG_DECODE_FUSED (the default
+ * where the model and device allow it: 4 query heads, context_length <=
+ * 4096, 256 compute units) runs a whole forward pass -- and, for a
+ * vocabulary that is a multiple of 16384, the LM head and the selection --
+ * as one launch of a persistent kernel whose 256 blocks hand their outputs
+ * to each other in device memory; GG_DECODE_GRAPH replays one kernel per
+ * phase (133 per 1B token). Both compute the same functions; summation
+ * orders differ. The environment variable GG_DECODE=graph selects the
+ * graph path when gg_set_decode_path was not called. No counterpart in the
+ * reference (engine.ts:735-802 encodes one dispatch per kernel). */
+#define GG_DECODE_GRAPH 0
+#define GG_DECODE_FUSED 1
+int gg_set_decode_path(gg_ctx* ctx, int32_t path);   /* before gg_finalize */
+int gg_decode_path(gg_ctx* ctx);                      /* after gg_finalize: the path in use */
+/* Profiling: with GG_DEC_TIMELINE=1 in the environment at gg_finalize the
+ * persistent kernel stamps the s_memrealtime clock (100 MHz) at 16 phase
+ * events per (block, layer); this copies the last launch's stamps,
+ * [256][layers][16] int64 (0 = not reached by that block). */
+int gg_decode_timeline(gg_ctx* ctx, int64_t* dst, size_t n);
+
 /* Message for the last failing call on ctx (or of gg_create when ctx is NULL). */
 const char* gg_last_error(const gg_ctx* ctx);
 

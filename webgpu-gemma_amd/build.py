@@ -16,7 +16,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 from scalar code.
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["gg_kernels.hip", "gg_runtime.hip"]
+SOURCES = ["gg_kernels.hip", "gg_decode.hip", "gg_runtime.hip"]
 
 
 def _run(cmd, cwd=None):

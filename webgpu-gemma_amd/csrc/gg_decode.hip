@@ -1,0 +1,868 @@
+// gg_decode.hip -- the persistent decode kernel: one launch per token.
+//
+// The per-kernel token loop (gg_kernels.hip) pays a dependent kernel launch
+// for each of its 133 phases per token (2.4-3.7 us each on MI355X, measured
+// in a graph-replay chain), and each kernel starts its weight stream only
+// after its launch. Here 256 co-resident blocks (one per CU, 8 waves each)
+// run every phase of every layer in one launch and hand outputs over through
+// LL words: a 64-bit {f32 value, 32-bit tag} pair written and polled with
+// device-scope relaxed atomics (global_store/load ... sc1). A word is valid
+// when its tag equals the (launch, layer) tag, so a consumer needs no flag,
+// no counter and no fence; an agent-scope release/acquire fence (a whole-L2
+// write-back or invalidate on this multi-XCD part) cost 32 us per phase in a
+// 256-block exchange, the LL exchange 2.2-2.5 us (1152 words) and 3.3 us
+// (6912 words). A block issues the weight loads of its next phase before it
+// polls that phase's input, so the weight stream overlaps the hand-off.
+//
+// Phases per layer (engine.ts:766-795 order):
+//   Q   blocks [0, 192): 8-row groups of the fused QKV GEMV. Every block
+//       first rebuilds the residual stream from the previous layer's down
+//       output (post-FFN norm + residual, engine.ts:794) into its own LDS:
+//       the residual is never exchanged, each block keeps an identical copy.
+//   A   blocks [192, 256): decode attention, block = (chunk of the span,
+//       query head), 16 chunks per head (fusedPerHeadNormRope, kvCacheStore,
+//       attnScore/softmax/attnOutput, shaders.ts:209-325); chunk 0's block
+//       of each head merges the head's 16 chunk partials.
+//   O   blocks [0, H / 8): attention output projection.
+//   F1  all blocks: post-attention norm + residual + ffn_norm, gate/up GEMV,
+//       GeGLU (engine.ts:785-792).
+//   F2  blocks [0, H / 8): down projection (engine.ts:793).
+// Then DEC_FWD: block 0 finishes the pass (output norm, engine.ts:794-801);
+// DEC_STEP: every block takes one vocabulary class c (rows c + 256 k, the
+// stride classes of argmax / topk256, shaders.ts:327-384) of the tied LM
+// head, from a class-major copy of the embedding, and hands over its
+// class candidate; block 0 selects the token (engine.ts:805-902).
+//
+// Every wait is bounded (a_spin_limit of s_memrealtime ticks): a block that
+// times out raises the host-visible flag and leaves, so the launch always
+// ends (the hand-off needs all 256 blocks resident: one per CU).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "gg_device.h"
+#include "gg_internal.h"
+
+namespace gg {
+namespace {
+
+constexpr int NT = kDecThreads;
+constexpr int NW = kDecThreads / 64;
+constexpr int kEPT = 2048 / NT;     // residual elements per thread (H <= 2048)
+constexpr int kNifGu = (kDecMaxH / 64 + NW - 1) / NW;  // gate/up items per wave (one 64-row group, Kp = H / 64)
+constexpr int kDR = (kDecMaxH + NT - 1) / NT;           // W_down rows per thread
+
+// Thread / block index as values the compiler cannot hoist out of the layer
+// loop: loop-invariant addresses and offsets derived from them would stay
+// live in registers across every phase of the loop.
+__device__ __forceinline__ int tidx() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int bidx() {
+  int b = blockIdx.x;
+  asm volatile("" : "+s"(b));
+  return b;
+}
+
+__device__ __forceinline__ uint64_t ll_ld(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_st(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ll_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ bool ll_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+
+// Thread t polls words t + NT k (k < PER) until each of its words below n
+// carries `tag` (buffers hold NT * PER words, so every load of a round is
+// issued unconditionally before any is checked). Returns false on timeout.
+template <int PER>
+__device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag, float* v, long long limit) {
+  const int tid = tidx();
+  const char* sb = (const char*)src;
+  const long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    uint64_t w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) w[k] = ll_ld((const uint64_t*)(sb + (uint32_t)(8 * (tid + NT * k))));
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) ok = ok && (tid + NT * k >= n || ll_ok(w[k], tag));
+    if (ok) {
+#pragma unroll
+      for (int k = 0; k < PER; ++k) v[k] = ll_val(w[k]);
+      return true;
+    }
+    if (__builtin_amdgcn_s_memrealtime() - t0 > limit) return false;
+  }
+}
+
+// Sum over the block (NW waves, fixed order); `sh` holds NW floats and must
+// not be reused before the next barrier.
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  v = wave_sum_dpp(v);
+  const int id = tidx();
+  if ((id & 63) == 0) sh[id >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += sh[w];
+  return t;
+}
+
+// ---- block-level Q8_0 GEMV over item-planar row groups ----------------------
+// Items [i0, i0 + ni) (row groups g0.. of KpS items each) split evenly over
+// the 8 waves; every load is issued with clamped indices (exact wait counts).
+template <int CI, int NIF>
+__device__ __forceinline__ void mg_issue(const uint8_t* W, int Kp, int KpS, int i0, int ni, Pair* w) {
+  constexpr int GR = 64 / CI;
+  const int t = tidx(), lane = t & 63, wv = t >> 6, cp = lane / GR;
+  const int wi0 = i0 + (wv * ni) / NW, wi1 = i0 + ((wv + 1) * ni) / NW;
+#pragma unroll
+  for (int k = 0; k < NIF; ++k) {
+    const int it = max(min(wi0 + k, wi1 - 1), i0);
+    const int sp = it % KpS;
+    // lanes of a padding column phase load the phase-0 lane of their row
+    const int ll = sp * CI + cp < Kp ? lane : (lane & (GR - 1));
+    load_planes_g(gmem(W) + (size_t)it * kColBytes, ll, w[k]);
+  }
+}
+
+// Dot products of the wave's items against x (LDS, kXPad layout); row sums of
+// each touched group land in red[wave][row - g0 * GR] (red zeroed before).
+template <int CI, int NIF>
+__device__ __forceinline__ void mg_dots(const Pair* w, const float* xs, int Kp, int KpS, int g0, int i0, int ni,
+                                        float (*red)[kDecMaxRows]) {
+  constexpr int GR = 64 / CI;
+  const int t = tidx(), lane = t & 63, wv = t >> 6, cp = lane / GR;
+  const int wi0 = i0 + (wv * ni) / NW, wi1 = i0 + ((wv + 1) * ni) / NW;
+  float acc = 0.f;
+  int gcur = wi0 / KpS - g0;
+  auto flush = [&](int gl) {
+    float v = acc;
+#pragma unroll
+    for (int m = GR; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+    if (lane < GR) red[wv][gl * GR + lane] = v;
+  };
+#pragma unroll
+  for (int k = 0; k < NIF; ++k) {
+    const int it = wi0 + k;
+    const int g = it / KpS, s = it - g * KpS;
+    const int c = s * CI + cp;
+    float d = dot_pair(w[k], xs + min(c, Kp - 1) * kXPad, 0.f);
+    d = (c < Kp && it < wi1) ? d : 0.f;
+    if (it < wi1 && g - g0 != gcur) {
+      flush(gcur);
+      gcur = g - g0;
+      acc = 0.f;
+    }
+    acc += d;
+  }
+  if (wi1 > wi0) flush(gcur);
+}
+
+__device__ __forceinline__ void zero_red(float (*red)[kDecMaxRows]) {
+  for (int i = tidx(); i < NW * kDecMaxRows; i += NT) (&red[0][0])[i] = 0.f;
+}
+
+__device__ __forceinline__ float red_row(const float (*red)[kDecMaxRows], int t) {
+  float r = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) r += red[w][t];
+  return r;
+}
+
+struct Smem {
+  float4 xs4[kMaxK / 64 * kXPad / 4];   // GEMV input x (K <= 8192)
+  float res[2048];                      // residual stream (H <= 2048), identical in every block
+  float red[NW][kDecMaxRows];
+  float shw[2][NW];
+  int fail;
+  float4 qs4[64], ks4[64], vs4[64];     // attention: normed + roped q, k; v
+  float4 wo[NW][64];
+  float wm[NW], wl[NW];
+  float act[32];                        // the FFN block's GeGLU outputs
+  float cand_v[NW];
+  uint32_t cand_i[NW];
+  SelShared sel;
+};
+
+// Timeline stamp (profiling builds of a step only): thread 0 of each block
+// records s_memrealtime at event ev of layer l.
+__device__ __forceinline__ void stamp(const DecodeArgs& a, int b, int l, int ev) {
+  if (a.timeline && tidx() == 0)
+    a.timeline[((size_t)b * a.L + l) * kDecEvents + ev] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void report_timeout(const DecodeArgs& a) {
+  if (tidx() == 0)
+    __hip_atomic_store(a.host_out + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Block-uniform failure check after a poll (one barrier).
+__device__ __forceinline__ bool failed(Smem& S, bool ok) {
+  if (!ok) S.fail = 1;
+  __syncthreads();
+  return S.fail != 0;
+}
+
+// residual = pre_res + rmsNorm(v) * w (fusedNormAdd, shaders.ts:386-418) for
+// this thread's elements e = tid + NT i < H; returns sum of r^2 over the block.
+__device__ __forceinline__ void resid_update(Smem& S, const float* v, const float* w, int H, float eps, float* r,
+                                             int shi) {
+  const int tid = tidx();
+  float s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i)
+    if (tid + NT * i < H) s1 = fmaf(v[i], v[i], s1);
+  const float ri1 = rsq(block_sum(s1, S.shw[shi]) / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const int e = tid + NT * i;
+    if (e < H) {
+      r[i] = S.res[e] + (v[i] * w[i]) * ri1;
+      S.res[e] = r[i];
+    }
+  }
+}
+
+// This thread's elements e = tid + NT i < H of a norm weight vector, loaded
+// before the poll they follow so that their latency overlaps the hand-off.
+__device__ __forceinline__ void load_norm(const float* w, int H, float* dst) {
+  const int tid = tidx();
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) dst[i] = gmem(w)[min(tid + NT * i, H - 1)];
+}
+
+// x = rmsNorm(r) * w into the GEMV input (rmsNorm, shaders.ts:25-56).
+__device__ __forceinline__ void norm_to_xs(Smem& S, const float* r, const float* w, int H, float eps, int shi) {
+  const int tid = tidx();
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i)
+    if (tid + NT * i < H) ss = fmaf(r[i], r[i], ss);
+  const float ri = rsq(block_sum(ss, S.shw[shi]) / (float)H + eps);
+  float* xs = (float*)S.xs4;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const int e = tid + NT * i;
+    if (e < H) xs[xs_index(e)] = (r[i] * w[i]) * ri;
+  }
+}
+
+// Poll n <= NT * PER LL words into the GEMV input x.
+template <int PER>
+__device__ __forceinline__ bool poll_to_xs(Smem& S, const uint64_t* src, int n, uint32_t tag, long long lim) {
+  float v[PER];
+  const bool ok = ll_wait<PER>(src, n, tag, v, lim);
+  float* xs = (float*)S.xs4;
+  if (ok) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int e = tidx() + NT * k;
+      if (e < n) xs[xs_index(e)] = v[k];
+    }
+  }
+  return ok;
+}
+
+// ---- attention block: chunk c of head h (16 chunks per head) ---------------
+// Wave w runs passes of 8 positions t0 + 64 p + 8 w + i; lane (i, o) =
+// (lane / 8, lane % 8) holds key dims 4 (o + 8 j) .. +3, lane l value dims
+// 4 l .. 4 l + 3; online softmax in base 2 (scores scaled by log2(e) / 16).
+// Layer l's tensors, formed from the slab bases and strides.
+struct LayerView {
+  const uint8_t *qkv, *o, *guf, *dcb;
+  const float* norms;      // norm j at norms + j * norm_stride
+  float *kc, *vc;
+  const float* rope;
+  int window;
+};
+__device__ __forceinline__ LayerView layer_view(const DecodeArgs& a, int l) {
+  LayerView v;
+  v.qkv = a.w_qkv + (size_t)l * a.st_qkv;
+  v.o = a.w_o + (size_t)l * a.st_o;
+  v.guf = a.w_guf + (size_t)l * a.st_guf;
+  v.dcb = a.w_dcb + (size_t)l * a.st_dcb;
+  v.norms = a.norms + (size_t)l * 6 * a.norm_stride;
+  v.kc = a.kc + (size_t)l * a.kv_stride;
+  v.vc = a.vc + (size_t)l * a.kv_stride;
+  const bool swa = (l % a.swa_period) < a.swa_period - 1;
+  v.rope = swa ? a.rope_local : a.rope_global;
+  v.window = swa ? a.window : 0;
+  return v;
+}
+__device__ __forceinline__ const float* norm_of(const DecodeArgs& a, const LayerView& v, int j) {
+  return v.norms + (size_t)j * a.norm_stride;
+}
+
+__device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, const LayerView& Ly, int l, int c,
+                                                int h, int pos, uint32_t tag) {
+  const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
+  const long long lim = a.spin_limit;
+  int t_lo, ch, nch;
+  dec_span(pos, Ly.window, kDecChunks, &t_lo, &ch, &nch);
+  uint64_t* part = a.x_part + (size_t)(h * kDecChunks + c) * kDecPart;
+  if (c >= nch) {   // past the span: an empty partial (m = -inf)
+    for (int d = tid; d < kDecPart; d += NT) ll_st(part + d, d == kHeadDim ? -INFINITY : 0.f, tag);
+    return true;
+  }
+  const int t0 = t_lo + c * ch;
+  const int t1 = min(t0 + ch, pos + 1);
+  const int npass = (t1 - t0 + 8 * NW - 1) / (8 * NW);
+  const int kv_last = max(pos - 1, 0);   // cache rows [0, pos) hold earlier tokens
+  const int pl = lane >> 3, oc = lane & 7;
+  const bool holder = (c == nch - 1);
+  float4 kr[8], vr[8];
+  auto load_k = [&](int p) {
+    const int t = min(t0 + 8 * NW * p + 8 * wv + pl, kv_last);
+    const GG_GLOBAL f32x4* kp = (const GG_GLOBAL f32x4*)(gmem(Ly.kc) + (size_t)t * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 v = __builtin_nontemporal_load(kp + oc + 8 * j);
+      kr[j] = make_float4(v.x, v.y, v.z, v.w);
+    }
+  };
+  auto load_v = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = min(t0 + 8 * NW * p + 8 * wv + i, kv_last);
+      const f32x4 v = __builtin_nontemporal_load((const GG_GLOBAL f32x4*)(gmem(Ly.vc) + (size_t)t * kHeadDim) + lane);
+      vr[i] = make_float4(v.x, v.y, v.z, v.w);
+    }
+  };
+  // K/V rows of the first pass and the RoPE row go out before the q/k/v poll
+  load_k(0);
+  load_v(0);
+  const GG_GLOBAL float* rt = gmem(Ly.rope) + (size_t)pos * kHeadDim;
+  float cs[2], sn[2], nw[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cs[j] = rt[lane + 64 * j];
+    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
+  }
+  const GG_GLOBAL float* wnorm = gmem(norm_of(a, Ly, wv == 1 ? 3 : 2));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) nw[i] = wnorm[lane + 64 * i];
+  // wave 0: q of head h; holder wave 1: this token's k, wave 2: its v
+  bool ok = true;
+  float hx[4];
+  if (wv == 0 || (holder && wv <= 2)) {
+    const uint64_t* src = a.x_qkv + (wv == 0 ? h * kHeadDim : a.QD + (wv - 1) * kHeadDim);
+    const long long st0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      uint64_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = ll_ld(src + (wv == 2 ? 4 * lane + i : lane + 64 * i));
+      bool good = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) good = good && ll_ok(w[i], tag);
+      if (good) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hx[i] = ll_val(w[i]);
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - st0 > lim) { ok = false; break; }
+    }
+  }
+  // QK-norm + NEOX RoPE (fusedPerHeadNormRope): lane owns dims lane + 64 i
+  auto norm_rope = [&](float* x, float4* dst4) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
+    ss = wave_sum_dpp(ss);
+    const float ri = rsq(ss / (float)kHeadDim + a.eps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (x[i] * nw[i]) * ri;
+    float* dst = (float*)dst4;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float x0 = x[j], x1 = x[j + 2];
+      dst[lane + 64 * j] = x0 * cs[j] - x1 * sn[j];
+      dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
+    }
+  };
+  if (ok) {
+    if (wv == 0) norm_rope(hx, S.qs4);
+    if (holder && wv == 1) norm_rope(hx, S.ks4);
+    if (holder && wv == 2) S.vs4[lane] = make_float4(hx[0], hx[1], hx[2], hx[3]);
+  }
+  if (failed(S, ok)) return false;
+  stamp(a, blockIdx.x, l, 12);
+  if (holder && h == 0 && tid < kHeadDim) {
+    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
+    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
+  }
+  if (c == 0 && tid < 64) *(float4*)(a.q_dbg + (size_t)l * a.QD + h * kHeadDim + 4 * tid) = S.qs4[tid];
+
+  float4 qr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qr[j] = S.qs4[oc + 8 * j];
+  const float sl2 = a.attn_scale * 1.4426950408889634f;
+  float m = -INFINITY, lsum = 0.f;
+  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p = 0; p < npass; ++p) {
+    const int tb = t0 + 8 * NW * p + 8 * wv;
+    const int t = tb + pl;
+    if (t == pos) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kr[j] = S.ks4[oc + 8 * j];
+    }
+    float d = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      d = fmaf(qr[j].x, kr[j].x, d);
+      d = fmaf(qr[j].y, kr[j].y, d);
+      d = fmaf(qr[j].z, kr[j].z, d);
+      d = fmaf(qr[j].w, kr[j].w, d);
+    }
+    d = group8_sum(d);
+    const float sc = t < t1 ? d * sl2 : -INFINITY;
+    if (p + 1 < npass) load_k(p + 1);
+    const float mx = across8_max(sc);
+    const float mn = fmaxf(m, mx);
+    const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+    const float pr = (sc == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc - mn);
+    lsum = fmaf(lsum, alpha, across8_sum(pr));
+    m = mn;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (tb + i == pos) vr[i] = S.vs4[lane];
+    o4.x *= alpha;
+    o4.y *= alpha;
+    o4.z *= alpha;
+    o4.w *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), 8 * i));
+      o4.x = fmaf(pv, vr[i].x, o4.x);
+      o4.y = fmaf(pv, vr[i].y, o4.y);
+      o4.z = fmaf(pv, vr[i].z, o4.z);
+      o4.w = fmaf(pv, vr[i].w, o4.w);
+    }
+    if (p + 1 < npass) load_v(p + 1);
+  }
+  // merge the eight waves (fixed order) into the chunk's (max, sum, o)
+  S.wo[wv][lane] = o4;
+  if (lane == 0) {
+    S.wm[wv] = m;
+    S.wl[wv] = lsum;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float M = S.wm[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, S.wm[w]);
+    float L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = S.wm[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(S.wm[w] - M);
+      L = fmaf(f, S.wl[w], L);
+      const float4 v = S.wo[w][tid];
+      O.x = fmaf(f, v.x, O.x);
+      O.y = fmaf(f, v.y, O.y);
+      O.z = fmaf(f, v.z, O.z);
+      O.w = fmaf(f, v.w, O.w);
+    }
+    ll_st(part + 4 * tid, O.x, tag);
+    ll_st(part + 4 * tid + 1, O.y, tag);
+    ll_st(part + 4 * tid + 2, O.z, tag);
+    ll_st(part + 4 * tid + 3, O.w, tag);
+    if (tid == 0) {
+      ll_st(part + kHeadDim, M, tag);
+      ll_st(part + kHeadDim + 1, L, tag);
+    }
+  }
+  return true;
+}
+
+// Chunk 0's block of head h: merge the head's 16 chunk partials,
+// o = sum_c f_c o_c / sum_c f_c l_c with f_c = 2^(m_c - max m) (maxima in
+// log2 units; empty chunks have m_c = -inf), into the O GEMV's input.
+// Threads 0..31 poll the (m, l) words, threads 0..255 one dim of each o_c.
+__device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, int h, uint32_t tag) {
+  const int tid = tidx();
+  const uint64_t* base = a.x_part + (size_t)h * kDecChunks * kDecPart;
+  bool ok = true;
+  float oc[kDecChunks];
+  if (tid < kHeadDim) {
+    const long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      uint64_t wo[kDecChunks];
+#pragma unroll
+      for (int c = 0; c < kDecChunks; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
+      const int si = min(tid, 2 * kDecChunks - 1);   // (m, l) word of threads < 32
+      const uint64_t ws = ll_ld(base + (si >> 1) * kDecPart + kHeadDim + (si & 1));
+      bool good = tid >= 2 * kDecChunks || ll_ok(ws, tag);
+#pragma unroll
+      for (int c = 0; c < kDecChunks; ++c) good = good && ll_ok(wo[c], tag);
+      if (good) {
+#pragma unroll
+        for (int c = 0; c < kDecChunks; ++c) oc[c] = ll_val(wo[c]);
+        if (tid < 2 * kDecChunks) S.red[0][tid] = ll_val(ws);
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_limit) { ok = false; break; }
+    }
+  }
+  if (failed(S, ok)) return false;
+  stamp(a, blockIdx.x, l, 13);
+  if (tid < kHeadDim) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kDecChunks; ++c) M = fmaxf(M, S.red[0][2 * c]);
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < kDecChunks; ++c) {
+      const float f = __builtin_amdgcn_exp2f(S.red[0][2 * c] - M);
+      L = fmaf(f, S.red[0][2 * c + 1], L);
+      acc = fmaf(f, oc[c], acc);
+    }
+    const float x = acc * (1.f / L);
+    ll_st(a.x_attn + h * kHeadDim + tid, x, tag);
+    if (l == a.L - 1) a.attn_out[h * kHeadDim + tid] = x;
+  }
+  return true;
+}
+
+}  // namespace
+
+template <int MODE>
+__global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
+  __shared__ Smem S;
+  const int tid = threadIdx.x, b = blockIdx.x;
+  const int H = a.H;
+  const long long lim = a.spin_limit;
+  if (tid == 0) S.fail = 0;
+  const DevState* st = a.st;
+  const uint32_t epoch = st->epoch;
+  const int pos = st->pos;
+  const int cur = st->cursor;
+  const int token = cur < 0 ? st->token : a.tokens[cur];
+  const uint32_t base = epoch * (uint32_t)(a.L + 2);
+  __syncthreads();
+
+  const int Kq = H / 64;
+  float r[kEPT];
+  // layer 0's residual stream: the embedding row (shaders.ts:2-23)
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const int e = tid + NT * i;
+    if (e < H) {
+      r[i] = embed_value(a.embd, a.kps_embd, a.embed_scale, token, e);
+      S.res[e] = r[i];
+    }
+  }
+
+  for (int l = 0; l < a.L; ++l) {
+    const int tid = tidx(), b = bidx();
+    const LayerView Ly = layer_view(a, l);
+    const uint32_t tag = base + (uint32_t)l + 1;
+    stamp(a, b, l, 0);
+    // ---- Q: residual stream update in every block; QKV rows in [0, 192) ----
+    const bool qb = b < kDecQBlocks;
+    const bool ffb = b < a.g_f;                     // this block runs the FFN block b
+    Pair wq[1], wg[kNifGu];
+    uint32_t dq[kDR][8];                            // W_down input block b: 32 int8 of rows tid + NT i
+    uint16_t dsc[kDR];                              // and their f16 scales
+    float wn[kEPT];
+    // the FFN weights are issued as soon as the block's Q or A work is done:
+    // they stream in while attention runs and the O hand-off waits
+    auto issue_ffn = [&]() {
+      if (!ffb) return;
+      mg_issue<1, kNifGu>(Ly.guf, Kq, Kq, b * Kq, Kq, wg);
+      const GG_GLOBAL uint8_t* col = gmem(Ly.dcb) + (size_t)b * 34 * H;
+#pragma unroll
+      for (int i = 0; i < kDR; ++i) {
+        const int rr = min(tid + NT * i, H - 1);
+        const GG_GLOBAL u32x4* q4 = (const GG_GLOBAL u32x4*)(col + 2 * H + 32 * rr);
+        const u32x4 q0 = __builtin_nontemporal_load(q4), q1 = __builtin_nontemporal_load(q4 + 1);
+        dq[i][0] = q0.x; dq[i][1] = q0.y; dq[i][2] = q0.z; dq[i][3] = q0.w;
+        dq[i][4] = q1.x; dq[i][5] = q1.y; dq[i][6] = q1.z; dq[i][7] = q1.w;
+        dsc[i] = ((const GG_GLOBAL uint16_t*)col)[rr];
+      }
+    };
+    if (qb) mg_issue<8, 1>(Ly.qkv, Kq, a.kps_qkv, b * a.kps_qkv, a.kps_qkv, wq);
+    if (qb) load_norm(norm_of(a, Ly, 0), H, wn);
+    if (l > 0) {
+      float dv[kEPT], wpost[kEPT];
+      load_norm(norm_of(a, layer_view(a, l - 1), 5), H, wpost);
+      const bool ok = ll_wait<kEPT>(a.x_down, H, tag - 1, dv, lim);
+      if (failed(S, ok)) { report_timeout(a); return; }
+      stamp(a, b, l, 1);
+      resid_update(S, dv, wpost, H, a.eps, r, 0);
+      if (b == 0) {
+#pragma unroll
+        for (int i = 0; i < kEPT; ++i)
+          if (tid + NT * i < H) a.hist[(size_t)(l - 1) * H + tid + NT * i] = r[i];
+      }
+    }
+    if (qb) {
+      zero_red(S.red);
+      norm_to_xs(S, r, wn, H, a.eps, 1);
+      __syncthreads();
+      stamp(a, b, l, 8);
+      mg_dots<8, 1>(wq, (const float*)S.xs4, Kq, a.kps_qkv, b, b * a.kps_qkv, a.kps_qkv, S.red);
+      __syncthreads();
+      if (tid < 8) ll_st(a.x_qkv + 8 * b + tid, red_row(S.red, tid), tag);
+      stamp(a, b, l, 2);
+      issue_ffn();
+    } else {
+      // ---- A: attention (blocks [192, 256)) ----
+      const int ab = b - kDecQBlocks;
+      const int c = (ab & 7) + 8 * (ab >> 5), h = (ab >> 3) & 3;
+      if (!attention_block(a, S, Ly, l, c, h, pos, tag)) { report_timeout(a); return; }
+      stamp(a, b, l, 2);
+      if (c == 0 && !merge_head(a, S, l, h, tag)) { report_timeout(a); return; }
+      if (c == 0) stamp(a, b, l, 3);
+      issue_ffn();
+    }
+    __syncthreads();
+
+    // ---- O: attention output projection (blocks [0, H / 8)) ----
+    if (b < a.g_o) {
+      Pair wo[1];
+      mg_issue<8, 1>(Ly.o, a.QD / 64, a.kps_o, b * a.kps_o, a.kps_o, wo);
+      zero_red(S.red);
+      const bool ok = poll_to_xs<kAttnMaxQ * kHeadDim / NT>(S, a.x_attn, a.QD, tag, lim);
+      if (failed(S, ok)) { report_timeout(a); return; }
+      stamp(a, b, l, 3);
+      mg_dots<8, 1>(wo, (const float*)S.xs4, a.QD / 64, a.kps_o, b, b * a.kps_o, a.kps_o, S.red);
+      __syncthreads();
+      if (tid < 8) ll_st(a.x_o + 8 * b + tid, red_row(S.red, tid), tag);
+      stamp(a, b, l, 4);
+      __syncthreads();
+    }
+
+    // ---- F: post-attention norm + residual + ffn_norm, then in block b < I / 32
+    // the gate/up rows of act[32 b .. 32 b + 31] (GeGLU) and that act slice
+    // times W_down's 32-wide input block b: a partial down output ----
+    {
+      zero_red(S.red);
+      float ov[kEPT], wpa[kEPT], wffn[kEPT];
+      load_norm(norm_of(a, Ly, 4), H, wpa);
+      load_norm(norm_of(a, Ly, 1), H, wffn);
+      const bool ok = ll_wait<kEPT>(a.x_o, H, tag, ov, lim);
+      if (failed(S, ok)) { report_timeout(a); return; }
+      stamp(a, b, l, 5);
+      resid_update(S, ov, wpa, H, a.eps, r, 0);
+      norm_to_xs(S, r, wffn, H, a.eps, 1);
+      __syncthreads();
+      stamp(a, b, l, 9);
+      if (ffb) {
+        mg_dots<1, kNifGu>(wg, (const float*)S.xs4, Kq, Kq, b, b * Kq, Kq, S.red);
+        __syncthreads();
+        stamp(a, b, l, 10);
+        // gate rows 0..31 of the group, the matching up rows 32..63
+        if (tid < 32) S.act[tid] = gelu_mul(red_row(S.red, tid), red_row(S.red, tid + 32));
+        __syncthreads();
+        // partial down output of this input block: (sum_k q[r][k] act[k]) * d_r
+        float act[32];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) act[k] = S.act[k];
+#pragma unroll
+        for (int i = 0; i < kDR; ++i) {
+          const int rr = tid + NT * i;
+          float sacc = 0.f;
+#pragma unroll
+          for (int k = 0; k < 32; ++k) sacc = fmaf(sbyte(dq[i][k >> 2], k & 3), act[k], sacc);
+          const float y = sacc * (float)__builtin_bit_cast(_Float16, dsc[i]);
+          if (rr < H) ll_st(a.x_dpart + (size_t)b * H + rr, y, tag);
+        }
+        stamp(a, b, l, 6);
+      }
+    }
+
+    // ---- R: down output rows 8 b .. 8 b + 7 = sum over the I / 32 partials ----
+    if (b < a.g_down) {
+      // thread t: row j = t / RT, partials m = t % RT + RT k, summed in
+      // increasing m, then a fixed-order reduction over the row's RT threads
+      constexpr int RT = NT / 8, PR = (kDecMaxFBlocks + RT - 1) / RT;
+      const int j = tid / RT, mt = tid % RT;
+      const uint64_t* src = a.x_dpart + 8 * b + j;
+      const long long t0 = __builtin_amdgcn_s_memrealtime();
+      float acc = 0.f;
+      bool ok = true;
+      for (;;) {
+        uint64_t w[PR];
+#pragma unroll
+        for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + RT * k, a.g_f - 1) * H);
+        bool good = true;
+#pragma unroll
+        for (int k = 0; k < PR; ++k) good = good && (mt + RT * k >= a.g_f || ll_ok(w[k], tag));
+        if (good) {
+#pragma unroll
+          for (int k = 0; k < PR; ++k)
+            if (mt + RT * k < a.g_f) acc += ll_val(w[k]);
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
+      }
+      if (failed(S, ok)) { report_timeout(a); return; }
+      stamp(a, b, l, 7);
+#pragma unroll
+      for (int m = 1; m < RT; m <<= 1) acc += __shfl_xor(acc, m, 64);
+      if (mt == 0) ll_st(a.x_down + 8 * b + j, acc, tag);
+      stamp(a, b, l, 11);
+    }
+    __syncthreads();
+  }
+
+  // ---- end of the pass: post-FFN norm + residual, output norm ----
+  const uint32_t tagL = base + (uint32_t)a.L;   // the last layer's down output
+  if (MODE == DEC_FWD && b != 0) return;
+  {
+    float dv[kEPT], wpost[kEPT], wout[kEPT];
+    load_norm(norm_of(a, layer_view(a, a.L - 1), 5), H, wpost);
+    load_norm(a.out_norm, H, wout);
+    const bool ok = ll_wait<kEPT>(a.x_down, H, tagL, dv, lim);
+    if (failed(S, ok)) { report_timeout(a); return; }
+    resid_update(S, dv, wpost, H, a.eps, r, 0);
+    norm_to_xs(S, r, wout, H, a.eps, 1);
+    __syncthreads();
+    if (b == 0) {
+      const float* xs = (const float*)S.xs4;
+#pragma unroll
+      for (int i = 0; i < kEPT; ++i) {
+        const int e = tid + NT * i;
+        if (e < H) {
+          a.hidden[e] = r[i];
+          a.hist[(size_t)(a.L - 1) * H + e] = r[i];
+          a.normed[e] = xs[xs_index(e)];
+        }
+      }
+    }
+  }
+  if (MODE == DEC_FWD) {
+    if (tid == 0) {
+      a.st->pos = pos + 1;
+      a.st->cursor = cur + 1;
+      a.st->epoch = epoch + 1;
+    }
+    return;
+  }
+
+  stamp(a, b, a.L - 1, 14);
+  // ---- LM head, vocabulary class b: rows b + 256 k, class-major copy ----
+  // Wave w takes the class's 64-row groups j = w + 4 q (q < kLmQ); lane =
+  // row, so each lane runs a whole row's dot product over its Kp items,
+  // streamed with kLmDepth items in flight per wave.
+  const int lane = tid & 63, wv = tid >> 6;
+  const int R = a.V / 256, R64 = R / 64;   // rows and 64-row groups per class
+  const int Kp = H / 64;
+  const int ngw = (R64 - wv + NW - 1) / NW;
+  const int nit = ngw * Kp;
+  auto item_ptr = [&](int i) {
+    const int q = i / Kp, cc = i - q * Kp;
+    const int P = b * R64 + wv + NW * q;
+    return a.lm + ((size_t)P * Kp + cc) * kColBytes;
+  };
+  const float* xs = (const float*)S.xs4;
+  constexpr int kLmDepth = 6;
+  // the class candidate: the first index of the maximum above -1e30, else
+  // (-1e30, 0) (strict >, shaders.ts:337-347); this lane's rows come in
+  // increasing index order (group q = 0, 1, ...)
+  float bv = -1e30f;
+  uint32_t bi = 0;
+  if (nit > 0) {
+    Pair p[kLmDepth];
+#pragma unroll
+    for (int d = 0; d < kLmDepth; ++d) load_planes(item_ptr(min(d, nit - 1)), lane, p[d]);
+    float acc = 0.f;
+    int q = 0, cc = 0;
+    for (int i = 0; i < nit; i += kLmDepth) {
+#pragma unroll
+      for (int d = 0; d < kLmDepth; ++d) {
+        const int it = i + d;
+        if (it < nit) {
+          acc = dot_pair(p[d], xs + cc * kXPad, acc);
+          if (++cc == Kp) {   // row group finished: logit (class-major) and candidate
+            const int j = wv + NW * q;
+            a.logits[(size_t)(b * R64 + j) * 64 + lane] = acc;
+            if (acc > bv) { bv = acc; bi = (uint32_t)(b + 256 * (64 * j + lane)); }
+            acc = 0.f;
+            cc = 0;
+            ++q;
+          }
+        }
+        if (it + kLmDepth < nit) load_planes(item_ptr(it + kLmDepth), lane, p[d]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const uint32_t oi = (uint32_t)__shfl_xor((int)bi, o, 64);
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) {
+    S.cand_v[wv] = bv;
+    S.cand_i[wv] = bi;
+  }
+  __syncthreads();
+  const uint32_t tagC = base + (uint32_t)a.L + 1;
+  stamp(a, b, a.L - 1, 15);
+  if (tid == 0) {
+    float v = S.cand_v[0];
+    uint32_t id = S.cand_i[0];
+    for (int w = 1; w < NW; ++w)
+      if (S.cand_v[w] > v || (S.cand_v[w] == v && S.cand_i[w] < id)) { v = S.cand_v[w]; id = S.cand_i[w]; }
+    ll_st(a.x_cand + 2 * b, v, tagC);
+    ll_st(a.x_cand + 2 * b + 1, __uint_as_float(id), tagC);
+  }
+  if (b != 0) return;
+
+  // ---- block 0: topk256 and the selection ----
+  float m = -1e30f;
+  uint32_t id = 0;
+  bool ok = true;
+  if (tid < 256) {
+    const long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      const uint64_t wv0 = ll_ld(a.x_cand + 2 * tid), wi0 = ll_ld(a.x_cand + 2 * tid + 1);
+      if (ll_ok(wv0, tagC) && ll_ok(wi0, tagC)) {
+        m = ll_val(wv0);
+        id = __float_as_uint(ll_val(wi0));
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
+    }
+  }
+  if (failed(S, ok)) { report_timeout(a); return; }
+  if (tid < 256) {
+    a.top[2 * tid] = __float_as_uint(m);
+    a.top[2 * tid + 1] = id;
+  }
+  const int tok = select_token(S.sel, m, id, tid < 256, st, a.seen, a.V);
+  if (tid == 0) {
+    a.st->out_token = tok;
+    a.host_out[0] = tok;
+    if (tok >= 0 && tok < a.V) {
+      a.seen[tok >> 5] |= 1u << (tok & 31);
+      a.st->seen_count += 1;
+    }
+    a.st->pos = pos + 1;
+    a.st->cursor = cur + 1;
+    a.st->epoch = epoch + 1;
+  }
+}
+
+int decode_occupancy() {
+  int n = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<DEC_STEP>, kDecThreads, 0);
+  return e == hipSuccess ? n : 0;
+}
+
+int launch_decode(int mode, const DecodeArgs& a, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (mode == DEC_STEP && !a.lm) return (int)hipErrorInvalidValue;
+  if (a.H > kDecMaxH || a.g_f > kDecMaxFBlocks) return (int)hipErrorInvalidValue;
+  if (mode == DEC_FWD) hipLaunchKernelGGL(k_decode<DEC_FWD>, dim3(kDecBlocks), dim3(kDecThreads), 0, s, a);
+  else hipLaunchKernelGGL(k_decode<DEC_STEP>, dim3(kDecBlocks), dim3(kDecThreads), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace gg

@@ -80,6 +80,7 @@ struct DevState {
   int32_t token;        // gg_step: the token to embed (cursor < 0)
   int32_t seen_count;   // number of ids added to the penalty bitmap
   int32_t out_token;    // last selected token
+  uint32_t epoch;       // launches of the persistent decode kernel so far (its hand-off tags)
 };
 
 struct GemvArgs {
@@ -208,6 +209,77 @@ struct SelectArgs {
   int32_t* host_out;       // optional: mapped pinned host word that also receives the token
 };
 
+// ---- persistent decode kernel (gg_decode.hip) -------------------------------
+// One launch runs a whole token: every layer's QKV, attention, O, gate/up and
+// down phases on 256 co-resident blocks (one per CU) that hand their outputs
+// over through "LL" words in device memory: 64-bit {f32 value, 32-bit tag}
+// written and polled with device-scope relaxed atomics, so a word carries its
+// own validity and no fence is needed. Tags are unique per (launch, layer).
+constexpr int kDecBlocks = 256;      // blocks of the persistent decode kernel
+constexpr int kDecThreads = 256;     // threads per block (4 waves, one per SIMD: 512 registers each)
+constexpr int kDecQBlocks = 192;     // QKV phase: blocks [0, 192), one 8-row group each (1536 rows)
+constexpr int kDecChunks = 16;       // attention chunks per head: blocks [192, 256) = 16 chunks x 4 heads
+constexpr int kDecPart = kHeadDim + 2;   // LL words of one chunk partial: o[256], m, l
+constexpr int kDecMaxRows = 128;     // rows of one phase a block may own
+constexpr int kDecMaxH = 1280;       // hidden sizes of the persistent kernel (its W_down rows per thread)
+constexpr int kDecMaxFBlocks = 256;  // FFN blocks: intermediate / 32 <= 256
+constexpr int kDecMaxCtx = 4096;     // 16 chunks per head cover spans up to 4096 positions
+enum DecMode { DEC_FWD = 0, DEC_STEP = 1 };
+
+// Every per-layer tensor kind is one layer-strided slab: layer l's copy is
+// at base + l * stride, formed from these arguments (scalar registers), so
+// the kernel never loads a pointer from memory in the middle of a phase.
+struct DecodeArgs {
+  const uint8_t* w_qkv;    // item-planar weights of every layer (CI = 8)
+  const uint8_t* w_o;
+  const uint8_t* w_guf;    // gate/up, CI = 1: 64-row group g = gate rows 32 g.. then up rows 32 g..
+  const uint8_t* w_dcb;    // down, column blocks: per 32-wide input block f16 scales [H], int8 [H][32]
+  size_t st_qkv, st_o, st_guf, st_dcb;   // bytes per layer
+  const float* norms;      // [L][6][norm_stride]: attn, ffn, q, k, post_attention, post_ffw
+  int norm_stride;
+  float* kc;               // [L][ctx][256]
+  float* vc;
+  size_t kv_stride;        // floats per layer (ctx * 256)
+  const float* rope_local; // [ctx][cos|sin][128]
+  const float* rope_global;
+  int swa_period;          // layer l is local when l % swa_period < swa_period - 1
+  int window;              // local layers' sliding window (0: full attention)
+  int L, H, I, QD, NQKV, V;
+  int kps_qkv, kps_o, kps_embd;
+  int g_f;                 // FFN blocks (intermediate / 32): block b < g_f takes act[32 b .. 32 b + 31]
+  int g_o, g_down;         // 8-row groups of O / of the down output: blocks [0, g) take one each
+  float eps, embed_scale, attn_scale;
+  const uint8_t* embd;     // tied embedding (CI = 1 layout, original row order)
+  const uint8_t* lm;       // DEC_STEP: the same rows class-major (row c + 256 k at c * V/256 + k)
+  const float* out_norm;
+  DevState* st;
+  const int32_t* tokens;
+  // hand-off buffers (LL words)
+  uint64_t* x_qkv;         // [NQKV]
+  uint64_t* x_part;        // [4][kDecChunks][kDecPart]
+  uint64_t* x_attn;        // [QD]
+  uint64_t* x_o;           // [H]
+  uint64_t* x_dpart;       // [g_f][H] partial down outputs
+  uint64_t* x_down;        // [H]
+  uint64_t* x_cand;        // [256][2]: per vocab class (value, id)
+  // parity outputs
+  float* hidden;
+  float* normed;
+  float* hist;             // [L][H]
+  float* q_dbg;            // [L][QD]
+  float* attn_out;         // [QD] (last layer)
+  float* logits;           // DEC_STEP: [V] class-major
+  uint32_t* top;           // [256] x {f32 bits, id}
+  uint32_t* seen;          // penalty bitmap
+  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag
+  long long spin_limit;    // s_memrealtime ticks (100 MHz) one hand-off may wait
+  long long* timeline;     // optional [256][L][kDecEvents] s_memrealtime stamps (null: off)
+};
+constexpr int kDecEvents = 16;  // timeline events per (block, layer)
+int launch_decode(int mode, const DecodeArgs& a, void* stream);
+// Blocks of the persistent kernel one CU can hold (it needs 1).
+int decode_occupancy();
+
 // ---- launchers (gg_kernels.hip) -------------------------------------------
 enum Prologue { PRO_NONE = 0, PRO_EMBED_NORM = 1, PRO_RESID_NORM = 2, PRO_ATTN_MERGE = 3 };
 enum Epilogue { EPI_OUT = 0, EPI_GEGLU = 1 };
@@ -225,6 +297,10 @@ int launch_select(const SelectArgs& a, void* stream);
 int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,
                   long long dst_row_offset, int interleave_half, void* stream);
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
+// GGUF Q8_0 rows -> column-block layout (per 32-wide block: f16 scales [rows], int8 [rows][32]).
+int launch_repack_colblock(const uint8_t* src, uint8_t* dst, long long rows, int K, void* stream);
+// Class-major copy of the CI = 1 LM head (rows a multiple of 16384).
+int launch_class_major(const uint8_t* src, uint8_t* dst, long long rows, int Kp, void* stream);
 // GGUF Q8_0 rows -> prefill GEMM weights: source row r to row r + off, or
 // with half = 16 to (r / 16) * 32 + r % 16 + off (gate: off 0, up: off 16).
 int launch_q8_bf16(const uint8_t* src, uint16_t* wb, float* wd, long long rows, int K, long long off, int half,

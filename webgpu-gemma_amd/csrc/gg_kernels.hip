@@ -35,189 +35,17 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "gg_device.h"
 #include "gg_internal.h"
 
 namespace gg {
 
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-
-constexpr int kXPad = 68;          // LDS floats per 64-wide x segment (4 pad: no bank conflicts)
-
-// ---------------------------------------------------------------------------
-// helpers
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float sbyte(uint32_t w, int b) {
-  // compiles to v_cvt_f32_i32_sdwa with a sign-extended byte select
-  return (float)(int8_t)(w >> (8 * b));
-}
-// 1 / sqrt(x) on v_rsq_f32 (about 1 ulp): every RMSNorm multiplies by it,
-// where the reference divides by sqrt(mean + eps) (shaders.ts:50-53, 415)
-__device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
-__device__ __forceinline__ float f16_lo(uint32_t w) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
-}
-__device__ __forceinline__ float f16_hi(uint32_t w) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-// Sum over a 256-thread block; every thread gets the same value.
-__device__ __forceinline__ float block_sum256(float v, float* sh4) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return ((sh4[0] + sh4[1]) + sh4[2]) + sh4[3];
-}
-
-__device__ __forceinline__ float block_max256(float v, float* sh4) {
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(sh4[0], sh4[1]), fmaxf(sh4[2], sh4[3]));
-}
-
-// Full-wave sum on the DPP network (no LDS round trips), the total
-// broadcast through lane 63: pairs, quads, half rows, rows, then the
-// row_bcast15 / row_bcast31 steps that fold rows 0-2 into row 3.
-template <int CTRL, int ROWMASK = 0xf>
-__device__ __forceinline__ float dpp_mov(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
-}
-__device__ __forceinline__ float wave_sum_dpp(float x) {
-  x += dpp_mov<0xB1>(x);         // quad_perm [1,0,3,2]
-  x += dpp_mov<0x4E>(x);         // quad_perm [2,3,0,1]
-  x += dpp_mov<0x141>(x);        // row_half_mirror
-  x += dpp_mov<0x140>(x);        // row_mirror
-  x += dpp_mov<0x142, 0xa>(x);   // row_bcast15 into rows 1 and 3
-  x += dpp_mov<0x143, 0xc>(x);   // row_bcast31 into rows 2 and 3
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-
-// DPP move whose rows outside ROWMASK read -inf (for max reductions).
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ float dpp_mov_ninf(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
-                                                               __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false));
-}
-// Sum over each aligned group of 8 lanes, result in all 8 (quad_perm xor 1,
-// xor 2, then row_half_mirror pairs the two quads).
-__device__ __forceinline__ float group8_sum(float x) {
-  x += dpp_mov<0xB1>(x);
-  x += dpp_mov<0x4E>(x);
-  x += dpp_mov<0x141>(x);
-  return x;
-}
-// Sum / max over the whole wave of values that are uniform within each group
-// of 8 lanes: row_mirror pairs the two groups of a row, the row_bcast15 /
-// row_bcast31 steps fold rows 0-2 into row 3, lane 63 is broadcast.
-__device__ __forceinline__ float across8_sum(float x) {
-  x += dpp_mov<0x140>(x);
-  x += dpp_mov<0x142, 0xa>(x);
-  x += dpp_mov<0x143, 0xc>(x);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-__device__ __forceinline__ float across8_max(float x) {
-  x = fmaxf(x, dpp_mov<0x140>(x));
-  x = fmaxf(x, dpp_mov_ninf<0x142, 0xa>(x));
-  x = fmaxf(x, dpp_mov_ninf<0x143, 0xc>(x));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-
-// One 68-byte pair = blocks 2c and 2c+1 of a row: 17 dwords.
-struct Pair {
-  uint32_t w[17];
-};
-
-// Lane `lane` of a wave loads slot `lane` of a 4352-byte item (item-planar
-// layout): four dwordx4 loads over 1024 contiguous bytes each, one dword load.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-// Weight items are read once per token: nontemporal loads (the `nt` bit)
-// keep them from displacing the activations, chunk partials and K/V rows
-// that the next kernels read from L2 (0.826 -> 0.789 ms per 1B token).
-__device__ __forceinline__ void load_planes(const uint8_t* item, int lane, Pair& P) {
-  const u32x4* p4 = (const u32x4*)item;
-  const u32x4 a = __builtin_nontemporal_load(p4 + lane), b = __builtin_nontemporal_load(p4 + 64 + lane),
-              c = __builtin_nontemporal_load(p4 + 128 + lane), d = __builtin_nontemporal_load(p4 + 192 + lane);
-  P.w[0] = a.x; P.w[1] = a.y; P.w[2] = a.z; P.w[3] = a.w;
-  P.w[4] = b.x; P.w[5] = b.y; P.w[6] = b.z; P.w[7] = b.w;
-  P.w[8] = c.x; P.w[9] = c.y; P.w[10] = c.z; P.w[11] = c.w;
-  P.w[12] = d.x; P.w[13] = d.y; P.w[14] = d.z; P.w[15] = d.w;
-  P.w[16] = __builtin_nontemporal_load((const uint32_t*)(item + 4096) + lane);
-}
-
-// acc += (sum_j q0[j] x[j]) * d0 + (sum_j q1[j] x[32+j]) * d1, each block sum
-// running over j in order like linearQ8 (shaders.ts:123-142). xc is 16-byte
-// aligned (LDS). Pair bytes: [0,2) d0 | [2,34) q0 | [34,36) d1 | [36,68) q1.
-__device__ __forceinline__ float dot_pair(const Pair& P, const float* __restrict__ xc, float acc) {
-  const float4* x4 = (const float4*)xc;
-  float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-  for (int j4 = 0; j4 < 8; ++j4) {
-    const float4 xv = x4[j4];
-    const int j = 4 * j4;
-    s0 = fmaf(sbyte(P.w[(2 + j) >> 2], (2 + j) & 3), xv.x, s0);
-    s0 = fmaf(sbyte(P.w[(3 + j) >> 2], (3 + j) & 3), xv.y, s0);
-    s0 = fmaf(sbyte(P.w[(4 + j) >> 2], (4 + j) & 3), xv.z, s0);
-    s0 = fmaf(sbyte(P.w[(5 + j) >> 2], (5 + j) & 3), xv.w, s0);
-  }
-#pragma unroll
-  for (int j4 = 0; j4 < 8; ++j4) {
-    const float4 xv = x4[8 + j4];
-    s1 = fmaf(sbyte(P.w[9 + j4], 0), xv.x, s1);
-    s1 = fmaf(sbyte(P.w[9 + j4], 1), xv.y, s1);
-    s1 = fmaf(sbyte(P.w[9 + j4], 2), xv.z, s1);
-    s1 = fmaf(sbyte(P.w[9 + j4], 3), xv.w, s1);
-  }
-  acc = fmaf(s0, f16_lo(P.w[0]), acc);
-  acc = fmaf(s1, f16_hi(P.w[8]), acc);
-  return acc;
-}
-
-// shaders.ts:153-170 (tanh GELU, argument clamped to +-15) times up.
-// 0.5 x (1 + tanh(arg)) = x / (1 + e^(-2 arg)), evaluated as
-// x * rcp(1 + 2^(-2 log2(e) arg)) on v_exp_f32 / v_rcp_f32 (a few ulp; the
-// tanh form loses the relative precision of 1 + tanh for negative arg).
-__device__ __forceinline__ float gelu_mul(float x, float up) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  float a = 1.0f + (k1 * x) * x;
-  float arg = (k0 * x) * a;
-  arg = fminf(fmaxf(arg, -15.0f), 15.0f);
-  const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg * -2.8853900817779268f));
-  return (x * sg) * up;
-}
-
-__device__ __forceinline__ int xs_index(int e) { return (e >> 6) * kXPad + (e & 63); }
 
 // ---------------------------------------------------------------------------
 // GEMV prologues: build the GEMV input x (K floats) in LDS.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float embed_elem(const GemvArgs& a, int token, int e) {
-  // shaders.ts:2-23: (f32(q) * scale) * sqrt(f32(H)), row `token` of the
-  // tied embedding (layout with CI = 1, GR = 64).
-  const int g = token >> 6, ln = token & 63;
-  const int b = e >> 5, c = b >> 1;
-  const uint8_t* item = a.embd + ((size_t)g * a.embd_KpS + c) * kColBytes;
-  // byte o of the pair: dword o / 4 of slot ln, byte o % 4
-  auto pb = [&](int o) { return item[plane_offset(o >> 2, ln) + (o & 3)]; };
-  const int off = (b & 1) ? 34 : 0;
-  const uint16_t sb = (uint16_t)(pb(off) | (pb(off + 1) << 8));
-  const float scale = (float)__builtin_bit_cast(_Float16, sb);
-  const float q = (float)(int8_t)pb(off + 2 + (e & 31));
-  const float t = q * scale;
-  return t * a.embed_scale;
+  return embed_value(a.embd, a.embd_KpS, a.embed_scale, token, e);
 }
 
 // Prologue inputs are read into registers before any reduction so that the
@@ -380,16 +208,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 // the wave's LDS slots, and a fixed-order sum over the waves gives the rows
 // (deterministic). Prologue reductions run on the DPP network.
 // ---------------------------------------------------------------------------
-// Decode attention chunking: the span split into at most mc (the launch's
-// chunk count) chunks of a multiple of 32 positions.
-__device__ __forceinline__ void dec_span(int pos, int window, int mc, int* t_lo, int* ch, int* nch) {
-  const int lo = window > 0 ? max(0, pos - window + 1) : 0;
-  const int span = pos - lo + 1;
-  const int c = kAttnChunk * ((span + kAttnChunk * mc - 1) / (kAttnChunk * mc));
-  *t_lo = lo;
-  *ch = c;
-  *nch = (span + c - 1) / c;
-}
 constexpr size_t kDecStatOff = (size_t)kDecMaxChunks * kAttnMaxQ * kHeadDim;   // (m, l) after the o block
 
 constexpr int kMgRows = 256;   // rows one block may own
@@ -1018,22 +836,8 @@ __global__ __launch_bounds__(256) void k_select1(SelectArgs a) {
   a.cand_id[blockIdx.x * 256 + tid] = id;
 }
 
-struct Cand {
-  double val;
-  int ord;
-  uint32_t id;
-};
-
-__device__ __forceinline__ bool cand_before(const Cand& x, const Cand& y) {
-  return x.val > y.val || (x.val == y.val && x.ord < y.ord);
-}
-
 __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
-  __shared__ float tv[256];
-  __shared__ uint32_t ti[256];
-  __shared__ Cand cs[256];
-  __shared__ float probs[256];
-  __shared__ int tok_sh;
+  __shared__ SelShared sh;
   const int tid = threadIdx.x;
   float m = -1e30f;
   uint32_t id = 0;
@@ -1049,76 +853,9 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
     for (int k = 0; k < 32; ++k)
       if (v[k] > m) { m = v[k]; id = ix[k]; }
   }
-  tv[tid] = m;
-  ti[tid] = id;
   a.top[2 * tid] = __float_as_uint(m);
   a.top[2 * tid + 1] = id;
-  __syncthreads();
-
-  const DevState* st = a.st;
-  const double T = st->temperature, rep = st->rep_penalty;
-  int token;
-  if (T == 0.0 && rep <= 1.0) {
-    for (int stride = 128; stride > 0; stride >>= 1) {
-      if (tid < stride && tv[tid + stride] > tv[tid]) {
-        tv[tid] = tv[tid + stride];
-        ti[tid] = ti[tid + stride];
-      }
-      __syncthreads();
-    }
-    token = (int)ti[0];
-  } else {
-    Cand cd;
-    cd.val = (double)m;
-    cd.ord = tid;
-    cd.id = id;
-    if (rep > 1.0 && st->seen_count > 0 && id < (uint32_t)a.V && ((a.seen[id >> 5] >> (id & 31)) & 1u)) {
-      if (cd.val > 0) cd.val /= rep;
-      else cd.val *= rep;
-    }
-    cs[tid] = cd;
-    __syncthreads();
-    for (int k = 2; k <= 256; k <<= 1) {
-      for (int jj = k >> 1; jj > 0; jj >>= 1) {
-        const int ixj = tid ^ jj;
-        if (ixj > tid) {
-          const bool up = (tid & k) == 0;
-          const Cand x = cs[tid], y = cs[ixj];
-          const bool sw = up ? cand_before(y, x) : cand_before(x, y);
-          if (sw) { cs[tid] = y; cs[ixj] = x; }
-        }
-        __syncthreads();
-      }
-    }
-    if (T == 0.0) {
-      token = (int)cs[0].id;
-    } else {
-      probs[tid] = (float)exp((cs[tid].val - cs[0].val) / T);
-      __syncthreads();
-      if (tid == 0) {
-        double sum = 0.0;
-        for (int i = 0; i < 256; ++i) sum += (double)probs[i];
-        double cum = 0.0;
-        int cutoff = 256;
-        for (int i = 0; i < 256; ++i) {
-          cum += (double)probs[i] / sum;
-          if (cum >= st->top_p) { cutoff = i + 1; break; }
-        }
-        double subset = 0.0;
-        for (int i = 0; i < cutoff; ++i) subset += (double)probs[i];
-        double r = st->u * subset;
-        int pick = -1;
-        for (int i = 0; i < cutoff; ++i) {
-          r -= (double)probs[i];
-          if (r <= 0) { pick = i; break; }
-        }
-        if (pick < 0) pick = cutoff - 1;
-        tok_sh = (int)cs[pick].id;
-      }
-      __syncthreads();
-      token = tok_sh;
-    }
-  }
+  const int token = select_token(sh, m, id, true, a.st, a.seen, a.V);
   if (tid == 0) {
     a.st->out_token = token;
     if (a.host_out) a.host_out[0] = token;
@@ -1731,6 +1468,42 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t* __restrict__ src,
   for (int i = 0; i < 17; ++i) *(uint32_t*)(item + plane_offset(i, slot)) = s[i];
 }
 
+// Class-major copy of a CI = 1 item-planar matrix (the tied LM head): row
+// c + 256 k (vocabulary stride class c, shaders.ts:337-347) goes to row
+// c * (rows / 256) + k, so each 64-row group of the copy holds one class.
+__global__ __launch_bounds__(256) void k_class_major(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                     long long rows, int Kp) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * Kp) return;
+  const long long r = idx / Kp;
+  const int c = (int)(idx - r * Kp);
+  const long long p = (r & 255) * (rows >> 8) + (r >> 8);
+  const uint8_t* si = src + ((size_t)(r >> 6) * Kp + c) * kColBytes;
+  uint8_t* di = dst + ((size_t)(p >> 6) * Kp + c) * kColBytes;
+  const int ss = (int)(r & 63), ds = (int)(p & 63);
+#pragma unroll
+  for (int i = 0; i < 17; ++i) *(uint32_t*)(di + plane_offset(i, ds)) = *(const uint32_t*)(si + plane_offset(i, ss));
+}
+
+// Column-block layout of a Q8_0 matrix (the down projection of the
+// persistent decode kernel): for each 32-wide input block m, the f16 scales
+// of all rows [rows], then their 32 int8 values [rows][32]: 34 * rows bytes
+// per block, so one block's column slice is contiguous.
+__global__ __launch_bounds__(256) void k_repack_colblock(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         long long rows, int nblk) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * nblk) return;
+  const long long r = idx / nblk;
+  const int m = (int)(idx - r * nblk);
+  const uint8_t* blk = src + (size_t)idx * 34;
+  uint8_t* col = dst + (size_t)m * 34 * rows;
+  col[2 * r] = blk[0];
+  col[2 * r + 1] = blk[1];
+  uint8_t* q = col + 2 * rows + 32 * r;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) q[i] = blk[2 + i];
+}
+
 // Bit-exact Q8_0 dequantisation of GGUF blocks (gguf.ts:107-124).
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, float* __restrict__ out,
                                                  long long n) {
@@ -1935,6 +1708,22 @@ int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long
   if (total <= 0) return 0;
   hipLaunchKernelGGL(k_repack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src,
                      dst, rows, L, off, half);
+  return (int)hipGetLastError();
+}
+
+int launch_repack_colblock(const uint8_t* src, uint8_t* dst, long long rows, int K, void* stream) {
+  if (rows <= 0 || K <= 0 || K % 32) return (int)hipErrorInvalidValue;
+  const long long total = rows * (K / 32);
+  hipLaunchKernelGGL(k_repack_colblock, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     src, dst, rows, K / 32);
+  return (int)hipGetLastError();
+}
+
+int launch_class_major(const uint8_t* src, uint8_t* dst, long long rows, int Kp, void* stream) {
+  if (rows <= 0 || rows % 16384 || Kp <= 0) return (int)hipErrorInvalidValue;
+  const long long total = rows * Kp;
+  hipLaunchKernelGGL(k_class_major, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src,
+                     dst, rows, Kp);
   return (int)hipGetLastError();
 }
 

@@ -88,6 +88,17 @@ struct gg_ctx {
   float* out_norm = nullptr;
   bool have_embd = false, have_out_norm = false;
   Q8Layout lay_embd{}, lay_qkv{}, lay_o{}, lay_gu{}, lay_down{};
+  // per-layer tensors of one kind live in one layer-strided slab, so a
+  // kernel forms layer l's address as base + l * stride from its arguments
+  uint8_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
+  float* s_norm = nullptr;            // [L][6][norm_stride]
+  int norm_stride = 0;
+  float *s_kc = nullptr, *s_vc = nullptr;   // [L][ctx][256]
+  // the persistent kernel's FFN copies: gate/up in 64-row groups (32 gate +
+  // the 32 matching up rows, CI = 1) and down in 32-wide column blocks
+  Q8Layout lay_guf{};
+  uint8_t *s_guf = nullptr, *s_dcb = nullptr;
+  size_t st_dcb = 0;
 
   // work buffers
   float *qkv_out = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_out = nullptr;
@@ -116,6 +127,19 @@ struct gg_ctx {
 
   hipGraphExec_t g_fwd = nullptr, g_sel = nullptr;
   hipGraphExec_t g_step = nullptr;   // state upload + forward + select: one launch per gg_step
+  // persistent decode kernel (gg_decode.hip): one launch per forward pass
+  int decode_req = -1;                // gg_set_decode_path; -1: GG_DECODE environment / default
+  bool fused = false;                 // forward passes run on the persistent kernel
+  bool fused_step = false;            // ... and so do the LM head and the selection of gg_step
+  std::string fused_why;              // why the persistent kernel is not used
+  uint64_t* xll = nullptr;            // its hand-off words
+  uint8_t* lm_cm = nullptr;           // class-major copy of the tied LM head
+  DecodeArgs dargs{};
+  hipGraphExec_t g_ffwd = nullptr, g_fstep = nullptr;
+  uint64_t dec_launches = 0;          // since the hand-off words were last cleared
+  size_t xll_words = 0;
+  bool logits_cm = false;             // the last logits are in class-major order
+  long long* timeline = nullptr;      // GG_DEC_TIMELINE=1: phase stamps of the last launch
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int probe_kind = GG_PROBE_NONE, probe_layer = 0;
   hipEvent_t probe_ev[4] = {nullptr, nullptr, nullptr, nullptr};   // kernel bracket [0, 1], empty bracket [2, 3]
@@ -199,6 +223,43 @@ struct ProbeScope {
     if (on) (void)hipEventRecordWithFlags(c->probe_ev[1], c->stream, hipEventRecordExternal);
   }
 };
+
+// Why the persistent decode kernel cannot run this model here ("" = it can).
+std::string fused_unsupported(gg_ctx* c) {
+  if (c->NQ != kAttnMaxQ) return "needs 4 query heads";
+  if (c->CTX > kDecMaxCtx) return "needs context_length <= 4096 (16 attention chunks per head)";
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, c->device) != hipSuccess || p.multiProcessorCount < kDecBlocks)
+    return "needs 256 compute units";
+  if (!c->s_guf) return "needs hidden <= 1280 and intermediate a multiple of 32 below 8193";
+  if (c->lay_qkv.KpS > 4 || c->lay_o.KpS > 4) return "items per block";
+  if (c->lay_qkv.rows / 8 != kDecQBlocks || c->lay_o.rows / 8 > kDecBlocks) return "row groups";
+  if (decode_occupancy() < 1) return "kernel does not fit one CU";
+  return "";
+}
+
+// Start a persistent-kernel launch: clear the hand-off words (and the
+// launch counter that feeds their tags) before the 32-bit tags could wrap.
+int fused_launch_begin(gg_ctx* c) {
+  const uint64_t limit = 0xffffffffull / (uint64_t)(c->L + 2) - 2;
+  if (c->dec_launches >= limit) {
+    GG_HIP(c, hipMemsetAsync(c->xll, 0, c->xll_words * 8, c->stream));
+    GG_HIP(c, hipMemsetAsync((char*)c->st + offsetof(DevState, epoch), 0, 4, c->stream));
+    c->dec_launches = 0;
+  }
+  c->dec_launches += 1;
+  return GG_OK;
+}
+
+int check_fused(gg_ctx* c) {
+  if (c->fused && c->h_out[1] != 0) {
+    c->lost = true;
+    return set_err(c, GG_ERR_DEVICE_LOST,
+                   "device lost: a hand-off of the persistent decode kernel timed out (its 256 blocks were not all "
+                   "resident)");
+  }
+  return GG_OK;
+}
 
 GemvArgs gemv_base(const uint8_t* W, const Q8Layout& L, float* out) {
   GemvArgs a{};
@@ -318,6 +379,10 @@ int record_forward_impl(gg_ctx* c, bool final_norm) {
 
 int record_forward(gg_ctx* c) { return record_forward_impl(c, true); }
 
+int record_fused_fwd(gg_ctx* c) {
+  return launch_rc(c, launch_decode(DEC_FWD, c->dargs, c->stream), "persistent decode kernel");
+}
+
 // Record LM head + selection (engine.ts:805-902). With `fused_final` the LM
 // head's prologue does k_final's work (post-FFN norm + residual, output norm,
 // hidden / normed / history stores and the position step, engine.ts:794-801)
@@ -384,7 +449,23 @@ int record_step(gg_ctx* c) {
   return record_select_impl(c, true);
 }
 
+// The same step on the persistent kernel: with a vocabulary that is a
+// multiple of 16384 its LM head and selection run in the same launch.
+int record_fused_step(gg_ctx* c) {
+  GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
+  if (c->fused_step)
+    return launch_rc(c, launch_decode(DEC_STEP, c->dargs, c->stream), "persistent decode kernel");
+  GG_TRY(record_fused_fwd(c));
+  return record_select(c);
+}
+
 int run_forward(gg_ctx* c) {
+  if (c->fused) {
+    GG_TRY(fused_launch_begin(c));
+    if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_ffwd, c->stream));
+    else GG_TRY(record_fused_fwd(c));
+    return GG_OK;
+  }
   if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
   else GG_TRY(record_forward(c));
   return GG_OK;
@@ -613,14 +694,25 @@ gg_ctx* gg_create(const gg_config* cfg) {
   c->lay_gu = q8_layout(2 * c->I, c->H, padfree_ci(c->H / 64));
   c->lay_down = q8_layout(c->H, c->I, 8);
   if (dalloc(c, &c->embd, c->lay_embd.bytes()) || dalloc(c, &c->out_norm, (size_t)c->H * 4)) return fail(0);
-  for (Layer& Ly : c->layers) {
-    if (dalloc(c, &Ly.qkv, c->lay_qkv.bytes()) || dalloc(c, &Ly.o, c->lay_o.bytes()) ||
-        dalloc(c, &Ly.gu, c->lay_gu.bytes()) || dalloc(c, &Ly.down, c->lay_down.bytes()))
-      return fail(0);
-    for (int j = 0; j < N_NNORM; ++j) {
-      const int n = (j == N_QN || j == N_KN) ? kHeadDim : c->H;
-      if (dalloc(c, &Ly.norm[j], (size_t)n * 4)) return fail(0);
-    }
+  c->norm_stride = c->H > kHeadDim ? c->H : kHeadDim;
+  if (dalloc(c, &c->s_qkv, c->L * c->lay_qkv.bytes()) || dalloc(c, &c->s_o, c->L * c->lay_o.bytes()) ||
+      dalloc(c, &c->s_gu, c->L * c->lay_gu.bytes()) || dalloc(c, &c->s_down, c->L * c->lay_down.bytes()) ||
+      dalloc(c, &c->s_norm, (size_t)c->L * N_NNORM * c->norm_stride * 4))
+    return fail(0);
+  // FFN copies of the persistent decode kernel, where its limits allow it
+  if (c->NQ == kAttnMaxQ && c->CTX <= kDecMaxCtx && c->H <= kDecMaxH && c->I % 32 == 0 &&
+      c->I / 32 <= kDecMaxFBlocks) {
+    c->lay_guf = q8_layout(2 * c->I, c->H, 1);
+    c->st_dcb = (size_t)(c->I / 32) * 34 * c->H;
+    if (dalloc(c, &c->s_guf, c->L * c->lay_guf.bytes()) || dalloc(c, &c->s_dcb, c->L * c->st_dcb)) return fail(0);
+  }
+  for (int l = 0; l < c->L; ++l) {
+    Layer& Ly = c->layers[l];
+    Ly.qkv = c->s_qkv + l * c->lay_qkv.bytes();
+    Ly.o = c->s_o + l * c->lay_o.bytes();
+    Ly.gu = c->s_gu + l * c->lay_gu.bytes();
+    Ly.down = c->s_down + l * c->lay_down.bytes();
+    for (int j = 0; j < N_NNORM; ++j) Ly.norm[j] = c->s_norm + ((size_t)l * N_NNORM + j) * c->norm_stride;
     if (c->c.prefill_batch > 0) {
       auto wcopy = [&](uint16_t** wb, float** wd, long long rows, long long K) {
         return dalloc(c, wb, (size_t)(rows * K * 2)) || dalloc(c, wd, (size_t)(rows * (K / 32) * 4));
@@ -725,6 +817,14 @@ int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t*
   }
   GG_HIP(c, hipMemcpy(c->staging, bytes, need, hipMemcpyHostToDevice));
   GG_TRY(launch_rc(c, launch_repack(c->staging, dst, *lay, rows, off, half, c->stream), "repack"));
+  if (layer >= 0 && c->s_guf) {
+    if (bit == Q_GATE || bit == Q_UP)
+      GG_TRY(launch_rc(c, launch_repack(c->staging, c->s_guf + layer * c->lay_guf.bytes(), c->lay_guf, rows,
+                                        bit == Q_UP ? 32 : 0, 32, c->stream), "repack"));
+    if (bit == Q_DOWN)
+      GG_TRY(launch_rc(c, launch_repack_colblock(c->staging, c->s_dcb + layer * c->st_dcb, rows, (int)K, c->stream),
+                       "repack"));
+  }
   if (layer >= 0 && c->c.prefill_batch > 0) {
     Layer& Ly = c->layers[layer];
     uint16_t* wb = nullptr;
@@ -760,11 +860,13 @@ int gg_finalize(gg_ctx* c) {
 
 
   const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
-  for (Layer& Ly : c->layers) {
-    GG_TRY(dalloc(c, &Ly.kc, kvb));
-    GG_TRY(dalloc(c, &Ly.vc, kvb));
-    GG_HIP(c, hipMemset(Ly.kc, 0, kvb));
-    GG_HIP(c, hipMemset(Ly.vc, 0, kvb));
+  GG_TRY(dalloc(c, &c->s_kc, kvb * c->L));
+  GG_TRY(dalloc(c, &c->s_vc, kvb * c->L));
+  GG_HIP(c, hipMemset(c->s_kc, 0, kvb * c->L));
+  GG_HIP(c, hipMemset(c->s_vc, 0, kvb * c->L));
+  for (int l = 0; l < c->L; ++l) {
+    c->layers[l].kc = c->s_kc + (size_t)l * c->CTX * kHeadDim;
+    c->layers[l].vc = c->s_vc + (size_t)l * c->CTX * kHeadDim;
   }
   GG_TRY(dalloc(c, &c->qkv_out, (size_t)c->NQKV * 4));
   // decode chunk partials: o [kDecMaxChunks][kAttnMaxQ][256], then (m, l)
@@ -836,6 +938,7 @@ int gg_finalize(gg_ctx* c) {
   GG_HIP(c, hipHostMalloc((void**)&c->h_tokens, (size_t)c->CTX * 4, hipHostMallocDefault));
   GG_HIP(c, hipHostMalloc((void**)&c->h_out, 64, hipHostMallocMapped | hipHostMallocCoherent));
   GG_HIP(c, hipHostGetDevicePointer((void**)&c->d_out, c->h_out, 0));
+  memset(c->h_out, 0, 64);
   memset(c->h_st, 0, sizeof(DevState));
   // timing events only: no system-scope fence (an L2 write-back) per record
   for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->ev[i], hipEventDisableSystemFence));
@@ -844,12 +947,102 @@ int gg_finalize(gg_ctx* c) {
     // around the bracketed launch
     for (int i = 0; i < 4; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->probe_ev[i], hipEventDisableSystemFence));
 
+  // persistent decode kernel: GG_DECODE=graph (or gg_set_decode_path) keeps
+  // the per-kernel graphs for every pass
+  if (c->decode_req < 0) {
+    const char* dm = getenv("GG_DECODE");
+    c->decode_req = (dm && strcmp(dm, "graph") == 0) ? GG_DECODE_GRAPH : GG_DECODE_FUSED;
+  }
+  c->fused_why = c->decode_req == GG_DECODE_FUSED ? fused_unsupported(c) : "graph path requested";
+  c->fused = c->decode_req == GG_DECODE_FUSED && c->fused_why.empty();
+  if (c->fused) {
+    DecodeArgs& d = c->dargs;
+    // hand-off words; polled buffers hold kDecThreads * (words per thread)
+    const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunks * kDecPart;
+    const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = 2048, w_dpart = (size_t)(c->I / 32) * c->H;
+    const size_t w_cand = 512;
+    c->xll_words = w_qkv + w_part + w_attn + 2 * w_h + w_dpart + w_cand;
+    GG_TRY(dalloc(c, &c->xll, c->xll_words * 8));
+    GG_HIP(c, hipMemset(c->xll, 0, c->xll_words * 8));
+    d.x_qkv = c->xll;
+    d.x_part = d.x_qkv + w_qkv;
+    d.x_attn = d.x_part + w_part;
+    d.x_o = d.x_attn + w_attn;
+    d.x_down = d.x_o + w_h;
+    d.x_dpart = d.x_down + w_h;
+    d.x_cand = d.x_dpart + w_dpart;
+    d.w_qkv = c->s_qkv;
+    d.w_o = c->s_o;
+    d.w_guf = c->s_guf;
+    d.w_dcb = c->s_dcb;
+    d.st_qkv = c->lay_qkv.bytes();
+    d.st_o = c->lay_o.bytes();
+    d.st_guf = c->lay_guf.bytes();
+    d.st_dcb = c->st_dcb;
+    d.norms = c->s_norm;
+    d.norm_stride = c->norm_stride;
+    d.kc = c->s_kc;
+    d.vc = c->s_vc;
+    d.kv_stride = (size_t)c->CTX * kHeadDim;
+    d.rope_local = c->rope_local;
+    d.rope_global = c->rope_global;
+    d.swa_period = c->c.swa_period;
+    d.window = c->c.sliding_window;
+    c->fused_step = c->V % 16384 == 0 && c->V <= 262144;
+    if (c->fused_step) {
+      GG_TRY(dalloc(c, &c->lm_cm, c->lay_embd.bytes()));
+      GG_TRY(launch_rc(c, launch_class_major(c->embd, c->lm_cm, c->V, c->lay_embd.Kp, c->stream), "class-major copy"));
+      GG_TRY(sync(c, "class-major copy"));
+    }
+    d.L = c->L;
+    d.H = c->H;
+    d.I = c->I;
+    d.QD = c->QD;
+    d.NQKV = c->NQKV;
+    d.V = c->V;
+    d.kps_qkv = c->lay_qkv.KpS;
+    d.kps_o = c->lay_o.KpS;
+    d.kps_embd = c->lay_embd.KpS;
+    d.g_f = c->I / 32;
+    d.g_o = c->lay_o.rows / 8;
+    d.g_down = c->lay_down.rows / 8;
+    d.eps = c->c.rms_norm_eps;
+    d.embed_scale = sqrtf((float)c->H);
+    d.attn_scale = (float)(1.0 / std::sqrt((double)kHeadDim));
+    d.embd = c->embd;
+    d.lm = c->lm_cm;
+    d.out_norm = c->out_norm;
+    d.st = c->st;
+    d.tokens = c->tokens;
+    d.hidden = c->hidden;
+    d.normed = c->normed;
+    d.hist = c->hist;
+    d.q_dbg = c->q_dbg;
+    d.attn_out = c->attn_out;
+    d.logits = c->logits;
+    d.top = c->top;
+    d.seen = c->seen;
+    d.host_out = c->d_out;
+    d.spin_limit = 2000000;   // 20 ms of s_memrealtime (100 MHz) per hand-off
+    // GG_DEC_TIMELINE=1: the persistent kernel stamps its phases (profiling)
+    const char* tl = getenv("GG_DEC_TIMELINE");
+    if (tl && tl[0] == '1') {
+      GG_TRY(dalloc(c, &d.timeline, (size_t)kDecBlocks * c->L * kDecEvents * 8));
+      GG_HIP(c, hipMemset(d.timeline, 0, (size_t)kDecBlocks * c->L * kDecEvents * 8));
+      c->timeline = d.timeline;
+    }
+  }
+
   const char* ng = getenv("GG_NO_GRAPH");
   c->use_graphs = !(ng && ng[0] == '1');
   if (c->use_graphs) {
     GG_TRY(capture(c, record_forward, &c->g_fwd));
     GG_TRY(capture(c, record_select, &c->g_sel));
     GG_TRY(capture(c, record_step, &c->g_step));
+    if (c->fused) {
+      GG_TRY(capture(c, record_fused_fwd, &c->g_ffwd));
+      GG_TRY(capture(c, record_fused_step, &c->g_fstep));
+    }
   }
   c->finalized = true;
   return GG_OK;
@@ -878,7 +1071,8 @@ int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
   }
   for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
   c->timed = c->probed = false;
-  return sync(c, "prefill");
+  GG_TRY(sync(c, "prefill"));
+  return check_fused(c);
 }
 
 static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bool with_forward) {
@@ -888,9 +1082,17 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   c->h_st->u = u;
   const bool ev = c->step_timing;   // three event records cost ~9 us of device time per step
   if (with_forward && !ev) {
-    if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
-    else GG_TRY(record_step(c));
+    if (c->fused) {
+      GG_TRY(fused_launch_begin(c));
+      if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
+      else GG_TRY(record_fused_step(c));
+    } else {
+      if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
+      else GG_TRY(record_step(c));
+    }
     GG_TRY(sync(c, "step"));
+    GG_TRY(check_fused(c));
+    c->logits_cm = c->fused_step;
     c->timed = false;
     c->probed = true;
     *out = c->h_out[0];
@@ -909,6 +1111,8 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (ev) GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
   // the selector stores the token straight into the mapped host word
   GG_TRY(sync(c, with_forward ? "step" : "select"));
+  GG_TRY(check_fused(c));
+  c->logits_cm = false;
   c->timed = ev;
   c->probed = true;
   *out = c->h_out[0];
@@ -986,6 +1190,17 @@ int gg_read(gg_ctx* c, int32_t what, int32_t layer, void* dst, size_t nbytes) {
   }
   if (nbytes < sz) sz = nbytes;
   GG_TRY(sync(c, "read"));
+  if (what == GG_READ_LOGITS && c->logits_cm) {
+    // the persistent kernel's LM head leaves class-major logits:
+    // row c + 256 k at c * (V / 256) + k
+    std::vector<float> cm((size_t)c->V);
+    GG_HIP(c, hipMemcpy(cm.data(), src, (size_t)c->V * 4, hipMemcpyDeviceToHost));
+    const int R = c->V / 256;
+    float* o = (float*)dst;
+    const size_t n = sz / 4;
+    for (size_t r = 0; r < n; ++r) o[r] = cm[(r & 255) * R + (r >> 8)];
+    return GG_OK;
+  }
   GG_HIP(c, hipMemcpy(dst, src, sz, hipMemcpyDeviceToHost));
   return GG_OK;
 }
@@ -1033,6 +1248,28 @@ int gg_probe_overhead(gg_ctx* c, float* ms) {
   return GG_OK;
 }
 
+int gg_set_decode_path(gg_ctx* c, int32_t path) {
+  if (!c) return GG_ERR_INVALID;
+  if (c->finalized) return set_err(c, GG_ERR_INVALID, "gg_set_decode_path must precede gg_finalize");
+  if (path != GG_DECODE_GRAPH && path != GG_DECODE_FUSED) return set_err(c, GG_ERR_INVALID, "unknown decode path");
+  c->decode_req = path;
+  return GG_OK;
+}
+
+int gg_decode_timeline(gg_ctx* c, int64_t* dst, size_t n) {
+  GG_TRY(check_ready(c));
+  if (!c->timeline || !dst) return set_err(c, GG_ERR_INVALID, "no timeline (GG_DEC_TIMELINE=1 at finalize)");
+  const size_t total = (size_t)kDecBlocks * c->L * kDecEvents;
+  GG_TRY(sync(c, "timeline"));
+  GG_HIP(c, hipMemcpy(dst, c->timeline, (n < total ? n : total) * 8, hipMemcpyDeviceToHost));
+  return GG_OK;
+}
+
+int gg_decode_path(gg_ctx* c) {
+  GG_TRY(check_ready(c));
+  return c->fused ? GG_DECODE_FUSED : GG_DECODE_GRAPH;
+}
+
 const char* gg_last_error(const gg_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
 
 void gg_destroy(gg_ctx* c) {
@@ -1041,6 +1278,8 @@ void gg_destroy(gg_ctx* c) {
   if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
   if (c->g_sel) (void)hipGraphExecDestroy(c->g_sel);
   if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
+  if (c->g_ffwd) (void)hipGraphExecDestroy(c->g_ffwd);
+  if (c->g_fstep) (void)hipGraphExecDestroy(c->g_fstep);
   for (hipEvent_t e : c->ev)
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->probe_ev)

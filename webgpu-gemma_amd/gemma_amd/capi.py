@@ -39,6 +39,10 @@ READ_V_CACHE = 6
 READ_Q = 7
 READ_ATTN_OUT = 8
 
+GG_DECODE_GRAPH = 0
+GG_DECODE_FUSED = 1
+DECODE_PATHS = {"graph": GG_DECODE_GRAPH, "fused": GG_DECODE_FUSED}
+
 PROBE = {"none": 0, "qkv": 1, "attn": 2, "o": 3, "gate_up": 4, "down": 5, "lm_head": 6, "select": 7}
 
 
@@ -97,6 +101,9 @@ _SIGS = {
     "gg_set_probe": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32]),
     "gg_probe_elapsed": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
     "gg_probe_overhead": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_float)]),
+    "gg_set_decode_path": (ctypes.c_int, [_P, ctypes.c_int32]),
+    "gg_decode_path": (ctypes.c_int, [_P]),
+    "gg_decode_timeline": (ctypes.c_int, [_P, _P, ctypes.c_size_t]),
     "gg_last_error": (ctypes.c_char_p, [_P]),
     "gg_destroy": (None, [_P]),
     "gg_q8_0_packed_size": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
@@ -161,6 +168,22 @@ class Engine:
     def upload_model(self, tensors: dict):
         for name, (t, dims, data) in tensors.items():
             self.upload(name, t, dims, data)
+
+    def set_decode_path(self, path: str):
+        """"fused" (persistent kernel) or "graph" (one kernel per phase); before finalize()."""
+        _check(self.ctx, lib().gg_set_decode_path(self.ctx, DECODE_PATHS[path]))
+
+    def decode_path(self) -> str:
+        rc = lib().gg_decode_path(self.ctx)
+        if rc < 0:
+            _check(self.ctx, rc)
+        return "fused" if rc == GG_DECODE_FUSED else "graph"
+
+    def decode_timeline(self) -> np.ndarray:
+        """[256, layers, 16] s_memrealtime stamps of the last persistent-kernel launch."""
+        out = np.zeros((256, self._cfg.num_layers, 16), dtype=np.int64)
+        _check(self.ctx, lib().gg_decode_timeline(self.ctx, out.ctypes.data, out.size))
+        return out
 
     def finalize(self):
         _check(self.ctx, lib().gg_finalize(self.ctx))
