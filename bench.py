@@ -85,10 +85,11 @@ def prefill_flops(shape, m: int):
 
 
 def prefill_report(shape, args, prefill_s: float) -> dict:
-    """TTFT and MFMA utilisation of the prefill. The GEMMs run two bf16 MFMA
-    passes (activation hi and lo parts) and attention's QK^T and PV three
-    (hi.hi, lo.hi, hi.lo), so the matrix-core time at peak is
-    (2 gemm + 3 attn) / bf16 peak; mfma_frac is that time over the TTFT."""
+    """TTFT and MFMA utilisation of the prefill. mfma_util is the algorithmic
+    FLOPs (GEMMs + causal attention) over TTFT over the dense bf16 peak.
+    The GEMMs run two bf16 MFMA passes (activation hi and lo parts) and
+    attention's QK^T and PV three (hi.hi, lo.hi, hi.lo): mfma_pass_frac is
+    that matrix-core work, (2 gemm + 3 attn) / bf16 peak, over the TTFT."""
     gemm, attn = prefill_flops(shape, args.ctx)
     out = {"tokens": args.ctx, "ttft_ms": round(prefill_s * 1e3, 2),
            "algorithmic_tflop": round((gemm + attn) / 1e12, 3),
@@ -101,8 +102,9 @@ def prefill_report(shape, args, prefill_s: float) -> dict:
                         "activations as bf16 hi + lo) + flash attention on bf16 MFMA (hi + lo splits of "
                         "q, k, p and v; three products)",
                 "gemm_tflop": round(gemm / 1e12, 3), "attention_tflop": round(attn / 1e12, 3),
-                "mfma_time_at_peak_ms": round(at_peak_s * 1e3, 3),
-                "mfma_frac": round(at_peak_s / prefill_s, 4)})
+                "mfma_util": round((gemm + attn) / prefill_s / (BF16_MFMA_PEAK_TFLOPS * 1e12), 4),
+                "mfma_pass_time_at_peak_ms": round(at_peak_s * 1e3, 3),
+                "mfma_pass_frac": round(at_peak_s / prefill_s, 4)})
     return out
 
 
@@ -122,10 +124,11 @@ def copy_calibration(nbytes: int):
     hip.hipFree(b)
 
 
-def measured_traffic():
-    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE and WRITE_SIZE, scaled by the copy calibration)."""
-    path = os.path.join(ROOT, "profiles", "gate_up_gemv_traffic.txt")
+def measured_traffic(name: str):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, scaled by the copy
+    calibration)."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch"):
@@ -169,6 +172,7 @@ def probe_kernel(shape, tensors, prompt, args):
     os.environ["GG_NO_GRAPH"] = "1"
     try:
         e = capi.Engine(shape.gg_config(prefill_batch=prefill_rows(args)))
+        e.set_decode_path("graph")
         e.set_probe(args.probe, args.probe_layer)
         e.upload_model(tensors)
         e.finalize()
@@ -211,6 +215,8 @@ def main():
                     help="rows per batched prefill slice (default: the whole context, at most 4096)")
     ap.add_argument("--token-prefill", action="store_true",
                     help="fill the context token by token (the reference's prefillBatched) instead of batched")
+    ap.add_argument("--decode", default="fused", choices=["fused", "graph"],
+                    help="decode path: the persistent kernel (one launch per token) or one kernel per phase")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the batch-1 token loop runs on "
@@ -230,8 +236,10 @@ def main():
     t_gen = time.perf_counter() - t0
     cfg = shape.gg_config(prefill_batch=prefill_rows(args))
     e = capi.Engine(cfg)
+    e.set_decode_path(args.decode)
     e.upload_model(tensors)
     e.finalize()
+    decode_path = e.decode_path()
     print(f"# model ready: generate {t_gen:.1f}s, upload {time.perf_counter() - t0 - t_gen:.1f}s", file=sys.stderr,
           flush=True)
 
@@ -272,17 +280,37 @@ def main():
     avg_bytes = float(np.mean([step_bytes(shape, p) for p in range(pos_timed0, pos_timed1)]))
     dev_ms = float(np.mean(fwd_ms))
 
-    # dominant-kernel timing: the same forward pass with its kernels launched
-    # directly on the engine's stream (the form rocprofv3 traces), HIP events
-    # recorded around the probed launch in every step of a timed loop, and an
-    # empty event pair recorded right before it for the events' own cost
-    probe = args.probe if args.probe != "none" else "gate_up"
-    k_bytes = kernel_bytes(shape, probe, pos_timed0)
-    bracket_ms = empty_ms = float("nan")
-    if args.probe != "none":
-        bracket_ms, empty_ms = probe_kernel(shape, tensors, prompt, args)
-    k_ms = bracket_ms
-    achieved = k_bytes / (k_ms * 1e-3) / 1e9
+    if decode_path == "fused":
+        # the persistent kernel is the whole token: one launch per gg_step,
+        # timed by the engine's step events (forward = the launch)
+        k_ms = dev_ms
+        k_bytes = int(avg_bytes)
+        roof = {"bound": "hbm", "kernel": "k_decode<DEC_STEP> (persistent: 26 layers + LM head + selection)",
+                "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("decode_step_traffic.txt"), "bytes_per_launch": k_bytes,
+                "avg_launch_us": round(k_ms * 1e3, 2), "launches": len(fwd_ms),
+                "timing": "HIP events around each graph launch of the step (state upload node + k_decode) over "
+                          f"{len(fwd_ms)} decode steps"}
+    else:
+        # dominant-kernel timing: the same forward pass with its kernels
+        # launched directly on the engine's stream (the form rocprofv3 traces),
+        # HIP events recorded around the probed launch in every step of a timed
+        # loop, and an empty event pair recorded right before it
+        probe = args.probe if args.probe != "none" else "gate_up"
+        k_bytes = kernel_bytes(shape, probe, pos_timed0)
+        bracket_ms = empty_ms = float("nan")
+        if args.probe != "none":
+            bracket_ms, empty_ms = probe_kernel(shape, tensors, prompt, args)
+        k_ms = bracket_ms
+        achieved = k_bytes / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": f"{args.probe} GEMV (layer {args.probe_layer})",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up_gemv_traffic.txt"),
+                "bytes_per_launch": k_bytes, "avg_launch_us": round(k_ms * 1e3, 2),
+                "empty_event_pair_us": round(empty_ms * 1e3, 2), "launches": args.probe_steps,
+                "timing": "HIP events around each direct launch of the kernel over a timed loop of "
+                          f"{args.probe_steps} decode steps"}
     out = {
         "metric": METRIC if args.ctx == 2048 else METRIC.replace("@ctx2k", f"@ctx{args.ctx}"),
         "value": round(value, 2),
@@ -299,14 +327,8 @@ def main():
         "config": {"workload": f"gemma3-1b-q8_0-greedy-decode-after-{args.ctx}", "ctx_prefilled": args.ctx,
                    "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
                    "gemma3 (22 local layers window 512 theta 1e4, 4 global theta 1e6)",
-                   "positions": [pos_timed0, pos_timed1 - 1]},
-        "roofline": {"bound": "hbm", "kernel": f"{args.probe} GEMV (layer {args.probe_layer})",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "bytes_per_launch": k_bytes, "avg_launch_us": round(k_ms * 1e3, 2),
-                     "empty_event_pair_us": round(empty_ms * 1e3, 2), "launches": args.probe_steps,
-                     "timing": "HIP events around each direct launch of the kernel over a timed loop of "
-                               f"{args.probe_steps} decode steps"},
+                   "positions": [pos_timed0, pos_timed1 - 1], "decode_path": decode_path},
+        "roofline": roof,
         "step_roofline": {"bytes_per_token": int(avg_bytes),
                           "achieved_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
                           "frac": round(avg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

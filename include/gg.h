@@ -50,6 +50,8 @@ extern "C" {
 #define GG_READ_V_CACHE 6       /* f32[ctx][256] V cache of layer `layer`      */
 #define GG_READ_Q 7             /* f32[n_q*256] normed+roped q of layer `layer` (last token) */
 #define GG_READ_ATTN_OUT 8      /* f32[n_q*256] attention output of the last layer */
+#define GG_READ_EMBED 9         /* f32[H]  embedding row of token `layer` (embeddingLookup, shaders.ts:2-23),
+                                   built by the device function both decode paths use */
 
 /* GemmaConfig (types.ts:2-36) plus the build's attention-mode fields. */
 typedef struct gg_config {
@@ -133,8 +135,10 @@ int gg_read(gg_ctx* ctx, int32_t what, int32_t layer, void* dst, size_t nbytes);
  * gg_select records three HIP events on the context's stream (about 9 us of
  * device time per step on MI355X), and gg_last_timing returns the last
  * call's forward and select time in milliseconds (GG_ERR_INVALID when timing
- * is off or no call has run since it was turned on). No counterpart in the
- * reference (WebGPU timestamp queries are not used in src/). */
+ * is off or no call has run since it was turned on). On the persistent
+ * decode path a gg_step is one launch: its whole time is reported as the
+ * forward time and the select time is 0. No counterpart in the reference
+ * (WebGPU timestamp queries are not used in src/). */
 int gg_set_timing(gg_ctx* ctx, int32_t on);
 int gg_last_timing(gg_ctx* ctx, float* forward_ms, float* select_ms);
 

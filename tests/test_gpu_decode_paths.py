@@ -1,0 +1,128 @@
+"""The two decode paths through the C-ABI: the persistent kernel (one launch
+per token, gg_decode.hip) and the per-kernel graph path compute the same
+functions -- checked against each other at the full 1B shape and against
+the oracle through the model tests -- plus the embedding row read back
+bit-exact and the persistent kernel's timeout report."""
+import os
+
+import numpy as np
+import pytest
+
+from gemma_amd import capi, synth
+from oracle import oracle as orc
+
+from gpu_util import rel, say
+
+pytestmark = pytest.mark.gpu
+
+
+def engine(shape, tensors, path=None, prefill_batch=0):
+    e = capi.Engine(shape.gg_config(prefill_batch=prefill_batch))
+    if path:
+        e.set_decode_path(path)
+    e.upload_model(tensors)
+    e.finalize()
+    return e
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    return synth.make_model(synth.TINY, seed=7)
+
+
+def test_decode_path_selection(gpu, tiny_model):
+    """The persistent kernel is the default where its limits hold (4 query
+    heads, context <= 4096); longer contexts keep the graph path."""
+    e = engine(synth.TINY.gemma3_mode(window=7), tiny_model)
+    assert e.decode_path() == "fused"
+    e.close()
+    e = engine(synth.TINY.with_ctx(8192).gemma3_mode(window=7), tiny_model)
+    assert e.decode_path() == "graph"
+    e.close()
+    e = engine(synth.TINY.gemma3_mode(window=7), tiny_model, "graph")
+    assert e.decode_path() == "graph"
+    e.close()
+
+
+@pytest.mark.parametrize("shape_name", ["tiny", "270m"])
+def test_embedding_row_bit_exact(gpu, tiny_model, shape_name):
+    """embeddingLookup (shaders.ts:2-23): (f32(q) * scale) * sqrt(f32(H)) of the
+    token's row, read through the device function both decode paths use,
+    bit-exact against the oracle for tokens 0, 1, 106 and V - 1."""
+    if shape_name == "tiny":
+        shape, t = synth.TINY, tiny_model
+    else:
+        shape = synth.GEMMA3_270M.gemma3_mode()
+        t = synth.make_model(shape, seed=270)
+    e = engine(shape, t)
+    emb = t["token_embd.weight"][2]
+    for tok in (0, 1, 106, shape.vocab - 1):
+        g = e.read(capi.READ_EMBED, tok)
+        r = orc.embed(emb, tok, shape.hidden)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), f"token {tok}"
+    e.close()
+
+
+@pytest.mark.parametrize("mode", ["gemma3", "reference"])
+def test_decode_paths_agree_1b(gpu, mode):
+    """Full 1B shape at context 4096: both paths over the same 320-token
+    prompt (token by token) and 24 greedy steps give the same tokens, every
+    layer's hidden state and the logits within 1e-4, and the same K/V rows."""
+    shape = synth.GEMMA3_1B.with_ctx(4096)
+    shape = shape.gemma3_mode() if mode == "gemma3" else shape.reference_mode()
+    say("1b paths build", mode)
+    t = synth.make_model(shape, seed=3)
+    prompt = synth.prompt_ids(320, seed=320, vocab=shape.vocab)
+    runs = {}
+    for path in ("fused", "graph"):
+        e = engine(shape, t, path)
+        assert e.decode_path() == path
+        e.prefill(prompt, 0)
+        tok = e.select()
+        toks, hid, logits = [tok], [], []
+        pos = len(prompt)
+        for step in range(24):
+            tok = e.step(tok, pos)
+            toks.append(tok)
+            pos += 1
+            if step % 8 == 7:
+                hid.append(np.stack([e.read(capi.READ_LAYER_HIDDEN, l) for l in range(shape.layers)]))
+                logits.append(e.read(capi.READ_LOGITS))
+        kv = [(e.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:pos],
+               e.read(capi.READ_V_CACHE, l).reshape(shape.ctx, 256)[:pos]) for l in (0, 5, 11, 25)]
+        runs[path] = (toks, hid, logits, kv)
+        say("1b path", path, "tokens", toks[:6])
+        e.close()
+    (ta, ha, la, ka), (tb, hb, lb, kb) = runs["fused"], runs["graph"]
+    assert ta == tb
+    for x, y in zip(ha, hb):
+        for l in range(shape.layers):
+            assert rel(x[l], y[l]) < 1e-4, f"layer {l}"
+    for x, y in zip(la, lb):
+        assert rel(x, y) < 1e-4
+    for (k1, v1), (k2, v2) in zip(ka, kb):
+        assert rel(k1, k2) < 1e-4 and rel(v1, v2) < 1e-4
+
+
+def test_persistent_kernel_timeout_is_reported(gpu, tiny_model, monkeypatch):
+    """Every hand-off wait of the persistent kernel is bounded; a wait that
+    runs out raises a host-visible flag and the block leaves, so the launch
+    ends and the call reports a lost device. Forced from the host with a
+    zero spin limit (the first unfinished poll gives up)."""
+    monkeypatch.setenv("GG_DEC_SPIN_LIMIT", "0")
+    shape = synth.TINY.gemma3_mode(window=7)
+    e = engine(shape, tiny_model, "fused")
+    monkeypatch.delenv("GG_DEC_SPIN_LIMIT")
+    with pytest.raises(capi.GGError) as ex:
+        for pos in range(4):
+            e.step(5, pos)
+    assert ex.value.code == capi.GG_ERR_DEVICE_LOST
+    assert "persistent decode kernel" in str(ex.value)
+    with pytest.raises(capi.GGError) as ex:
+        e.step(5, 0)
+    assert ex.value.code == capi.GG_ERR_DEVICE_LOST
+    e.close()
+    # a fresh context works
+    e = engine(shape, tiny_model, "fused")
+    e.step(5, 0)
+    e.close()

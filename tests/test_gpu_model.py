@@ -18,10 +18,14 @@ TOL = 1e-3
 _MODELS = {}
 
 
-def engine(shape, tensors):
+def engine(shape, tensors, path=None):
     e = capi.Engine(shape.gg_config())
+    if path:
+        e.set_decode_path(path)
     e.upload_model(tensors)
     e.finalize()
+    if path:
+        assert e.decode_path() == path
     return e
 
 
@@ -38,11 +42,12 @@ def tiny_model():
     return synth.make_model(synth.TINY, seed=7)
 
 
+@pytest.mark.parametrize("path", ["fused", "graph"])
 @pytest.mark.parametrize("mode", ["reference", "gemma3"])
-def test_tiny_greedy_loop(gpu, tiny_model, mode):
+def test_tiny_greedy_loop(gpu, tiny_model, mode, path):
     shape = synth.TINY.reference_mode() if mode == "reference" else synth.TINY.gemma3_mode(window=7)
-    say("tiny greedy", mode)
-    e = engine(shape, tiny_model)
+    say("tiny greedy", mode, path)
+    e = engine(shape, tiny_model, path)
     o = orc.OracleModel(shape, tiny_model)
     prompt = synth.prompt_ids(9, seed=11, vocab=shape.vocab)
     e.prefill(prompt, 0)
@@ -124,13 +129,14 @@ def test_tiny_sampling_stream(gpu, tiny_model):
     e.close()
 
 
-def test_270m_greedy_128(gpu):
+@pytest.mark.parametrize("path", ["fused", "graph"])
+def test_270m_greedy_128(gpu, path):
     """270M architecture, gemma3 mode: 64 seeded prompt ids then 128 greedy
     tokens, identical to the oracle; logits within 1e-3 at checkpoints."""
     shape = synth.GEMMA3_270M.gemma3_mode()
-    say("270m build")
+    say("270m build", path)
     t = synth.make_model(shape, seed=270)
-    e = engine(shape, t)
+    e = engine(shape, t, path)
     o = orc.OracleModel(shape, t)
     prompt = synth.prompt_ids(64, seed=64, vocab=shape.vocab)
     e.prefill(prompt, 0)

@@ -297,6 +297,8 @@ int launch_select(const SelectArgs& a, void* stream);
 int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long src_rows,
                   long long dst_row_offset, int interleave_half, void* stream);
 int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
+// One embedding row (embed_value) into out[H].
+int launch_embed_row(const uint8_t* embd, int kps, float scale, int token, int H, float* out, void* stream);
 // GGUF Q8_0 rows -> column-block layout (per 32-wide block: f16 scales [rows], int8 [rows][32]).
 int launch_repack_colblock(const uint8_t* src, uint8_t* dst, long long rows, int K, void* stream);
 // Class-major copy of the CI = 1 LM head (rows a multiple of 16384).

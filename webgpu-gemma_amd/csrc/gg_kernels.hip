@@ -1504,6 +1504,12 @@ __global__ __launch_bounds__(256) void k_repack_colblock(const uint8_t* __restri
   for (int i = 0; i < 32; ++i) q[i] = blk[2 + i];
 }
 
+// Embedding row of one token through embed_value (parity reads).
+__global__ __launch_bounds__(256) void k_embed_row(const uint8_t* embd, int kps, float scale, int token, int H,
+                                                   float* out) {
+  for (int e = threadIdx.x; e < H; e += 256) out[e] = embed_value(embd, kps, scale, token, e);
+}
+
 // Bit-exact Q8_0 dequantisation of GGUF blocks (gguf.ts:107-124).
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, float* __restrict__ out,
                                                  long long n) {
@@ -1708,6 +1714,11 @@ int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long
   if (total <= 0) return 0;
   hipLaunchKernelGGL(k_repack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src,
                      dst, rows, L, off, half);
+  return (int)hipGetLastError();
+}
+
+int launch_embed_row(const uint8_t* embd, int kps, float scale, int token, int H, float* out, void* stream) {
+  hipLaunchKernelGGL(k_embed_row, dim3(1), dim3(256), 0, (hipStream_t)stream, embd, kps, scale, token, H, out);
   return (int)hipGetLastError();
 }
 

@@ -104,6 +104,7 @@ struct gg_ctx {
   float *qkv_out = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_out = nullptr;
   float *act = nullptr, *down_out = nullptr, *hidden = nullptr, *residual = nullptr, *normed = nullptr;
   float *logits = nullptr, *hist = nullptr, *q_dbg = nullptr;
+  float* normed_tmp = nullptr;        // parity reads (GG_READ_EMBED)
   float *rope_local = nullptr, *rope_global = nullptr;   // [ctx][cos|sin][128]
   float* cand_val = nullptr;
   uint32_t *cand_id = nullptr, *top = nullptr, *seen = nullptr;
@@ -878,6 +879,7 @@ int gg_finalize(gg_ctx* c) {
   GG_TRY(dalloc(c, &c->hidden, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->residual, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->normed, (size_t)c->H * 4));
+  GG_TRY(dalloc(c, &c->normed_tmp, (size_t)c->H * 4));
   GG_TRY(dalloc(c, &c->logits, (size_t)c->V * 4));
   GG_TRY(dalloc(c, &c->hist, (size_t)c->L * c->H * 4));
   GG_TRY(dalloc(c, &c->q_dbg, (size_t)c->L * c->QD * 4));
@@ -1024,6 +1026,9 @@ int gg_finalize(gg_ctx* c) {
     d.seen = c->seen;
     d.host_out = c->d_out;
     d.spin_limit = 2000000;   // 20 ms of s_memrealtime (100 MHz) per hand-off
+    // GG_DEC_SPIN_LIMIT=<ticks>: a shorter bound (tests force the timeout path)
+    const char* sl = getenv("GG_DEC_SPIN_LIMIT");
+    if (sl && sl[0]) d.spin_limit = atoll(sl);
     // GG_DEC_TIMELINE=1: the persistent kernel stamps its phases (profiling)
     const char* tl = getenv("GG_DEC_TIMELINE");
     if (tl && tl[0] == '1') {
@@ -1094,6 +1099,23 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
     GG_TRY(check_fused(c));
     c->logits_cm = c->fused_step;
     c->timed = false;
+    c->probed = true;
+    *out = c->h_out[0];
+    return GG_OK;
+  }
+  if (with_forward && c->fused && c->fused_step) {
+    // timed persistent step: the whole token is one launch (forward, LM
+    // head and selection), reported as the forward time with select 0
+    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+    GG_TRY(fused_launch_begin(c));
+    if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
+    else GG_TRY(record_fused_step(c));
+    GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
+    GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
+    GG_TRY(sync(c, "step"));
+    GG_TRY(check_fused(c));
+    c->logits_cm = true;
+    c->timed = true;
     c->probed = true;
     *out = c->h_out[0];
     return GG_OK;
@@ -1186,6 +1208,13 @@ int gg_read(gg_ctx* c, int32_t what, int32_t layer, void* dst, size_t nbytes) {
       if (!lay_ok) return set_err(c, GG_ERR_INVALID, "layer out of range");
       src = c->q_dbg + (size_t)layer * c->QD; sz = (size_t)c->QD * 4; break;
     case GG_READ_ATTN_OUT: src = c->attn_out; sz = (size_t)c->QD * 4; break;
+    case GG_READ_EMBED:
+      if (layer < 0 || layer >= c->V) return set_err(c, GG_ERR_INVALID, "token out of range");
+      GG_TRY(launch_rc(c, launch_embed_row(c->embd, c->lay_embd.KpS, sqrtf((float)c->H), layer, c->H, c->normed_tmp,
+                                           c->stream), "embedding row"));
+      src = c->normed_tmp;
+      sz = (size_t)c->H * 4;
+      break;
     default: return set_err(c, GG_ERR_INVALID, "unknown read target");
   }
   if (nbytes < sz) sz = nbytes;

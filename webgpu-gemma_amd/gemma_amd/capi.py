@@ -38,6 +38,7 @@ READ_K_CACHE = 5
 READ_V_CACHE = 6
 READ_Q = 7
 READ_ATTN_OUT = 8
+READ_EMBED = 9
 
 GG_DECODE_GRAPH = 0
 GG_DECODE_FUSED = 1
@@ -225,6 +226,7 @@ class Engine:
                 READ_TOPK256: 512, READ_LAYER_HIDDEN: c.hidden_size,
                 READ_K_CACHE: c.context_length * c.head_dim, READ_V_CACHE: c.context_length * c.head_dim,
                 READ_Q: c.num_q_heads * c.head_dim, READ_ATTN_OUT: c.num_q_heads * c.head_dim,
+                READ_EMBED: c.hidden_size,
             }[what]
         out = np.empty(count, dtype=dtype)
         _check(self.ctx, lib().gg_read(self.ctx, what, layer, out.ctypes.data, out.nbytes))
