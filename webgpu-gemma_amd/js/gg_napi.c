@@ -14,9 +14,13 @@
  *   read(ctx, what, layer, typedArray)   debug readbacks
  *   destroy(ctx)                         dispose
  * prefill/select/step run on the libuv thread pool (napi_async_work) so the
- * JavaScript generate() loop stays asynchronous; the host serialises calls on
- * one context. Failures reject / throw an Error whose `code` is the GG_ERR_*
- * name; GG_ERR_DEVICE_LOST maps to the reference's deviceLost state.
+ * JavaScript generate() loop stays asynchronous. A context runs one call at a
+ * time: while a prefill/select/step is in flight every other call on that
+ * context throws / rejects with GG_ERR_INVALID ("busy"), and destroy() (or the
+ * garbage collector's finalizer) only marks the context; the last job's
+ * completion callback then calls gg_destroy, so a worker thread never runs on
+ * a destroyed context. Failures reject / throw an Error whose `code` is the
+ * GG_ERR_* name; GG_ERR_DEVICE_LOST maps to the reference's deviceLost state.
  */
 #include <node_api.h>
 #include <stdlib.h>
@@ -58,25 +62,52 @@ static napi_value throw_rc(napi_env env, gg_ctx* ctx, int rc) {
 }
 
 /* ---- argument helpers ---------------------------------------------------- */
+/* The JavaScript external's payload. Every field is read and written on the
+ * JavaScript thread only (binding calls, job completion, the finalizer); the
+ * worker thread sees the gg_ctx* copied into its job when the job was queued. */
 typedef struct {
-  gg_ctx* ctx;
+  gg_ctx* ctx;          /* NULL once destroyed */
+  int busy;             /* a prefill/select/step job is in flight */
+  int destroy_pending;  /* destroy() or the finalizer ran while busy */
+  int orphaned;         /* the finalizer ran: the job's completion frees this */
 } handle_t;
 
 static void finalize_handle(napi_env env, void* data, void* hint) {
   (void)env;
   (void)hint;
   handle_t* h = (handle_t*)data;
+  if (h->busy) {
+    h->destroy_pending = 1;
+    h->orphaned = 1;
+    return;
+  }
   if (h->ctx) gg_destroy(h->ctx);
   free(h);
 }
 
-static gg_ctx* get_ctx(napi_env env, napi_value v) {
+/* The handle behind argument v when it names a live context that is not
+ * running a job; otherwise throws GG_ERR_INVALID and returns NULL. */
+static handle_t* get_handle(napi_env env, napi_value v) {
   void* p = NULL;
-  if (napi_get_value_external(env, v, &p) != napi_ok || !p || !((handle_t*)p)->ctx) {
-    napi_throw_error(env, "GG_ERR_INVALID", "not a live engine context");
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
+    napi_throw_error(env, "GG_ERR_INVALID", "not an engine context");
     return NULL;
   }
-  return ((handle_t*)p)->ctx;
+  handle_t* h = (handle_t*)p;
+  if (!h->ctx || h->destroy_pending) {
+    napi_throw_error(env, "GG_ERR_INVALID", "the engine context was destroyed");
+    return NULL;
+  }
+  if (h->busy) {
+    napi_throw_error(env, "GG_ERR_INVALID", "the engine context is busy with another prefill/select/step call");
+    return NULL;
+  }
+  return h;
+}
+
+static gg_ctx* get_ctx(napi_env env, napi_value v) {
+  handle_t* h = get_handle(env, v);
+  return h ? h->ctx : NULL;
 }
 
 static int get_f64(napi_env env, napi_value obj, const char* key, double* out) {
@@ -151,7 +182,7 @@ static napi_value Create(napi_env env, napi_callback_info info) {
     int rc = (msg && strstr(msg, "device")) ? GG_ERR_NO_DEVICE : GG_ERR_INVALID;
     return throw_rc(env, NULL, rc);
   }
-  handle_t* h = (handle_t*)malloc(sizeof(handle_t));
+  handle_t* h = (handle_t*)calloc(1, sizeof(handle_t));
   if (!h) {
     gg_destroy(ctx);
     napi_throw_error(env, "GG_ERR_OOM", "host allocation failed");
@@ -278,10 +309,13 @@ static napi_value Destroy(napi_env env, napi_callback_info info) {
   void* p = NULL;
   CHECK(env, napi_get_value_external(env, argv[0], &p));
   handle_t* h = (handle_t*)p;
-  if (h && h->ctx) {
-    gg_destroy(h->ctx);
-    h->ctx = NULL;
+  if (!h || !h->ctx) return NULL;
+  if (h->busy) {
+    h->destroy_pending = 1;  /* the running job's completion destroys it */
+    return NULL;
   }
+  gg_destroy(h->ctx);
+  h->ctx = NULL;
   return NULL;
 }
 
@@ -289,6 +323,7 @@ static napi_value Destroy(napi_env env, napi_callback_info info) {
 enum { OP_PREFILL, OP_SELECT, OP_STEP };
 typedef struct {
   int op;
+  handle_t* h;
   gg_ctx* ctx;
   int32_t* ids;
   size_t n;
@@ -317,34 +352,56 @@ static void job_execute(napi_env env, void* data) {
   }
 }
 
+/* Runs on the JavaScript thread after job_execute. The handle is released
+ * (and a deferred destroy carried out) before the promise settles, because
+ * settling it may run the caller's continuation, which can start the next
+ * call on the same context. */
 static void job_complete(napi_env env, napi_status status, void* data) {
   job_t* j = (job_t*)data;
+  handle_t* h = j->h;
+  h->busy = 0;
+  if (h->destroy_pending && h->ctx) {
+    gg_destroy(h->ctx);
+    h->ctx = NULL;
+  }
+  if (h->orphaned) free(h);
+  napi_deferred d = j->deferred;
+  napi_value v;
+  int ok = 0;
   if (status != napi_ok) {
-    napi_reject_deferred(env, j->deferred, make_error(env, GG_ERR_INVALID, "job cancelled"));
+    v = make_error(env, GG_ERR_INVALID, "job cancelled");
   } else if (j->rc != GG_OK) {
-    napi_reject_deferred(env, j->deferred, make_error(env, j->rc, j->err));
+    v = make_error(env, j->rc, j->err);
   } else {
-    napi_value v;
+    ok = 1;
     if (j->op == OP_PREFILL) napi_get_undefined(env, &v);
     else napi_create_int32(env, j->out, &v);
-    napi_resolve_deferred(env, j->deferred, v);
   }
   napi_delete_async_work(env, j->work);
   free(j->ids);
   free(j);
+  if (ok) napi_resolve_deferred(env, d, v);
+  else napi_reject_deferred(env, d, v);
 }
 
-static napi_value queue_job(napi_env env, job_t* j) {
+/* Queues job j on handle h (live and idle, checked by get_handle) and marks
+ * h busy until job_complete runs. */
+static napi_value queue_job(napi_env env, handle_t* h, job_t* j) {
   napi_value promise, name;
+  j->h = h;
+  j->ctx = h->ctx;
+  j->work = NULL;
   if (napi_create_promise(env, &j->deferred, &promise) != napi_ok ||
       napi_create_string_utf8(env, "gg", NAPI_AUTO_LENGTH, &name) != napi_ok ||
       napi_create_async_work(env, NULL, name, job_execute, job_complete, j, &j->work) != napi_ok ||
       napi_queue_async_work(env, j->work) != napi_ok) {
+    if (j->work) napi_delete_async_work(env, j->work);
     free(j->ids);
     free(j);
     napi_throw_error(env, "GG_ERR_NAPI", "could not queue the call");
     return NULL;
   }
+  h->busy = 1;
   return promise;
 }
 
@@ -358,63 +415,60 @@ static int read_sample(napi_env env, napi_value* argv, job_t* j) {
 static napi_value Prefill(napi_env env, napi_callback_info info) {
   napi_value argv[3];
   if (!get_args(env, info, 3, argv)) return NULL;
-  gg_ctx* ctx = get_ctx(env, argv[0]);
-  if (!ctx) return NULL;
+  handle_t* h = get_handle(env, argv[0]);
+  if (!h) return NULL;
   job_t* j = (job_t*)calloc(1, sizeof(job_t));
   if (!j) {
     napi_throw_error(env, "GG_ERR_OOM", "host allocation failed");
     return NULL;
   }
   j->op = OP_PREFILL;
-  j->ctx = ctx;
   j->ids = copy_ids(env, argv[1], &j->n);
   if (!j->ids || napi_get_value_int32(env, argv[2], &j->pos) != napi_ok) {
     free(j->ids);
     free(j);
     return NULL;
   }
-  return queue_job(env, j);
+  return queue_job(env, h, j);
 }
 
 static napi_value Select(napi_env env, napi_callback_info info) {
   napi_value argv[5];
   if (!get_args(env, info, 5, argv)) return NULL;
-  gg_ctx* ctx = get_ctx(env, argv[0]);
-  if (!ctx) return NULL;
+  handle_t* h = get_handle(env, argv[0]);
+  if (!h) return NULL;
   job_t* j = (job_t*)calloc(1, sizeof(job_t));
   if (!j) {
     napi_throw_error(env, "GG_ERR_OOM", "host allocation failed");
     return NULL;
   }
   j->op = OP_SELECT;
-  j->ctx = ctx;
   if (!read_sample(env, argv + 1, j)) {
     free(j);
     napi_throw_type_error(env, "GG_ERR_INVALID", "sampling options must be numbers");
     return NULL;
   }
-  return queue_job(env, j);
+  return queue_job(env, h, j);
 }
 
 static napi_value Step(napi_env env, napi_callback_info info) {
   napi_value argv[7];
   if (!get_args(env, info, 7, argv)) return NULL;
-  gg_ctx* ctx = get_ctx(env, argv[0]);
-  if (!ctx) return NULL;
+  handle_t* h = get_handle(env, argv[0]);
+  if (!h) return NULL;
   job_t* j = (job_t*)calloc(1, sizeof(job_t));
   if (!j) {
     napi_throw_error(env, "GG_ERR_OOM", "host allocation failed");
     return NULL;
   }
   j->op = OP_STEP;
-  j->ctx = ctx;
   if (napi_get_value_int32(env, argv[1], &j->token) != napi_ok || napi_get_value_int32(env, argv[2], &j->pos) != napi_ok ||
       !read_sample(env, argv + 3, j)) {
     free(j);
     napi_throw_type_error(env, "GG_ERR_INVALID", "step arguments must be numbers");
     return NULL;
   }
-  return queue_job(env, j);
+  return queue_job(env, h, j);
 }
 
 static napi_value Init(napi_env env, napi_value exports) {
