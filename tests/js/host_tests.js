@@ -108,6 +108,8 @@ async function ggufTests() {
     assert.strictEqual(c.intermediate_size, expect.inter);
     assert.strictEqual(c.context_length, Math.min(expect.file_ctx, 4096));
     assert.strictEqual(c.vocab_size, expect.vocab);
+    assert.strictEqual(c.file_rope_theta, expect.rope_base);
+    assert.strictEqual(c.file_rope_theta_swa, expect.rope_base_swa);
     fs.closeSync(fd);
   });
 }
@@ -165,6 +167,45 @@ async function engineTests() {
     assert.strictEqual(cfg.vocab_size, expect.vocab);
     assert.strictEqual(cfg.context_length, 64);
     assert.strictEqual(gg.calls[gg.calls.length - 1][0], 'finalize');
+  });
+  await test('engine: model keys resolve to the reference\'s file names in modelDir', async () => {
+    const os = require('os');
+    const { MODEL_FILES } = require(path.join(JS, 'engine'));
+    assert.deepStrictEqual(Object.keys(MODEL_FILES).sort(), ['1b', '270m', 'func']);
+    const dir = fs.mkdtempSync(path.join(os.tmpdir(), 'gg-models-'));
+    try {
+      fs.symlinkSync(path.resolve(ggufPath), path.join(dir, 'gemma-3-270m-it-Q8_0.gguf'));
+      const gg = new FakeGG([]);
+      await createGemmaEngine({ model: '270m', modelDir: dir, backend: gg, contextLength: 64 });
+      assert.strictEqual(gg.calls[0][0], 'create');
+      await assert.rejects(createGemmaEngine({ model: '1b', modelDir: dir, backend: new FakeGG([]) }),
+        /model file not found: .*gemma-3-1b-it-Q8_0\.gguf/);
+      await assert.rejects(createGemmaEngine({ model: 'https://example.invalid/m.gguf', backend: new FakeGG([]) }),
+        /model URLs are not fetched/);
+      const saved = process.env.GEMMA_MODEL_DIR;
+      process.env.GEMMA_MODEL_DIR = dir;
+      try {
+        const gg2 = new FakeGG([]);
+        await createGemmaEngine({ model: '270m', backend: gg2, contextLength: 64 });
+        assert.strictEqual(gg2.calls[gg2.calls.length - 1][0], 'finalize');
+      } finally {
+        if (saved === undefined) delete process.env.GEMMA_MODEL_DIR;
+        else process.env.GEMMA_MODEL_DIR = saved;
+      }
+    } finally {
+      fs.unlinkSync(path.join(dir, 'gemma-3-270m-it-Q8_0.gguf'));
+      fs.rmdirSync(dir);
+    }
+  });
+  await test('engine: create() gets the file\'s rope bases (one base in reference mode)', async () => {
+    const ref = (await mk([])).gg.calls[0][1];
+    assert.strictEqual(ref.rope_theta_global, expect.rope_base);
+    assert.strictEqual(ref.rope_theta_local, expect.rope_base);
+    assert.strictEqual(ref.sliding_window, 0);
+    const g3 = (await mk([], { attention: 'gemma3' })).gg.calls[0][1];
+    assert.strictEqual(g3.rope_theta_global, expect.rope_base);
+    assert.strictEqual(g3.rope_theta_local, expect.rope_base_swa);
+    assert.strictEqual(g3.sliding_window, 512);
   });
   await test('engine: first turn prefill, first id from select, steps at kvPosition + writes, stop id', async () => {
     const { e, gg, draws } = await mk([210, 211, 212, 106]);

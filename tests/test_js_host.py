@@ -8,6 +8,7 @@ import json
 import os
 import shutil
 import subprocess
+from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -19,12 +20,14 @@ NODE = shutil.which("node")
 
 
 def write_tiny(path):
-    shape = synth.TINY
+    # rope bases other than the 1e6 / 1e4 defaults, so the test sees the file's values reach create()
+    shape = replace(synth.TINY, theta_global=5e5)
     tensors = synth.make_model(shape, seed=3)
-    synth.write_model_gguf(path, shape, tensors=tensors)
+    synth.write_model_gguf(path, shape, tensors=tensors, rope_base_swa=2e4)
     r = gguf.GGUFFile(path)
     exp = {"data_offset": r.data_offset, "hidden": shape.hidden, "layers": shape.layers, "inter": shape.inter,
-           "vocab": shape.vocab, "file_ctx": max(shape.ctx, 32768), "tensors": []}
+           "vocab": shape.vocab, "file_ctx": max(shape.ctx, 32768), "rope_base": 5e5, "rope_base_swa": 2e4,
+           "tensors": []}
     for t in r.tensors:
         b = np.ascontiguousarray(tensors[t.name][2]).tobytes()
         assert bytes(r.tensor_bytes(t)) == b

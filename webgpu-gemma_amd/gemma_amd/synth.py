@@ -13,7 +13,7 @@ from dataclasses import dataclass, replace
 import numpy as np
 
 from . import capi
-from .gguf import T_F32, T_Q8_0, V_ARRAY, V_STRING, V_UINT32, quantize_q8_0, q8_0_blocks, write_gguf
+from .gguf import T_F32, T_Q8_0, V_ARRAY, V_FLOAT32, V_STRING, V_UINT32, quantize_q8_0, q8_0_blocks, write_gguf
 
 Q8_NAMES = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
 NORM_NAMES = ["attn_norm", "ffn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm", "post_ffw_norm"]
@@ -127,8 +127,11 @@ def synthetic_vocab(vocab: int) -> list:
     return toks
 
 
-def write_model_gguf(path: str, shape: Shape, seed: int = 0, tensors: dict | None = None):
-    """A GGUF the reference parser accepts (gguf.ts:190-220 keys)."""
+def write_model_gguf(path: str, shape: Shape, seed: int = 0, tensors: dict | None = None,
+                     rope_base_swa: float | None = None):
+    """A GGUF the reference parser accepts (gguf.ts:190-220 keys), plus the
+    rope frequency base Gemma-3 files carry (shape.theta_global) and, when
+    given, a sliding-window layer base."""
     tensors = tensors if tensors is not None else make_model(shape, seed)
     kv = [
         ("general.architecture", V_STRING, "gemma3"),
@@ -140,6 +143,9 @@ def write_model_gguf(path: str, shape: Shape, seed: int = 0, tensors: dict | Non
         ("gemma3.attention.key_length", V_UINT32, shape.head_dim),
         ("gemma3.context_length", V_UINT32, max(shape.ctx, 32768)),
         ("gemma3.attention.sliding_window", V_UINT32, 512),
+        ("gemma3.rope.freq_base", V_FLOAT32, float(shape.theta_global)),
         ("tokenizer.ggml.tokens", V_ARRAY, (V_STRING, synthetic_vocab(shape.vocab))),
     ]
+    if rope_base_swa is not None:
+        kv.append(("gemma3.rope.freq_base_swa", V_FLOAT32, float(rope_base_swa)))
     write_gguf(path, kv, [(n, t, d, b) for n, (t, d, b) in tensors.items()])

@@ -26,6 +26,29 @@ function defaultConfig() {
   };
 }
 
+// The reference's model keys (engine.ts:24-28, options.model in types.ts:51)
+// name these Q8_0 files; with no network they are looked up in a local
+// directory (options.modelDir, else $GEMMA_MODEL_DIR, else the working
+// directory) instead of fetched. Any other model string is a file path.
+const MODEL_FILES = {
+  '1b': 'gemma-3-1b-it-Q8_0.gguf',
+  '270m': 'gemma-3-270m-it-Q8_0.gguf',
+  'func': 'functiongemma-270m-it-Q8_0.gguf',
+};
+
+function resolveModel(options) {
+  const key = options.model || '1b';
+  if (/^[a-z]+:\/\//i.test(key)) {
+    throw new Error('model URLs are not fetched: download the .gguf and pass its path, or a model key ' +
+                    'with modelDir: ' + key);
+  }
+  if (Object.prototype.hasOwnProperty.call(MODEL_FILES, key)) {
+    const dir = options.modelDir || process.env.GEMMA_MODEL_DIR || process.cwd();
+    return path.join(dir, MODEL_FILES[key]);
+  }
+  return key;
+}
+
 function loadBinding(dir) {
   const p = path.join(dir || path.join(__dirname, '..', 'lib'), 'gg_napi.node');
   return require(p);   // throws when the HIP library or the binding is missing
@@ -52,11 +75,11 @@ class GemmaEngineImpl {
     if (this.onProgress) this.onProgress({ loaded: loaded, total: total, status: status });
   }
 
-  // init(): the model is a path to a local .gguf file (no network here);
-  // tensors stream from the file to the device one at a time.
+  // init(): the model is a key of MODEL_FILES or the path of a local .gguf
+  // file; tensors stream from the file to the device one at a time.
   async init(options) {
-    const file = options.model;
-    if (!file || !fs.existsSync(file)) throw new Error('model must be the path of a .gguf file: ' + file);
+    const file = resolveModel(options);
+    if (!fs.existsSync(file)) throw new Error('model file not found: ' + file);
     const fd = fs.openSync(file, 'r');
     try {
       this.reportProgress(0, 1, 'Reading header...');
@@ -65,8 +88,15 @@ class GemmaEngineImpl {
       const emb = g.tensors.find((t) => t.name === 'token_embd.weight');
       if (!emb) throw new Error('GGUF has no token_embd.weight');
       cfg.vocab_size = emb.dims[1];
+      // The file's rope base replaces the 1e6 default of types.ts:32-33 on
+      // every layer (reference mode keeps one base, as types.ts does); in
+      // gemma3 mode local layers take the file's sliding-window base, else 1e4.
+      if (cfg.file_rope_theta) {
+        cfg.rope_theta_global = cfg.file_rope_theta;
+        cfg.rope_theta_swa = cfg.file_rope_theta;
+      }
       if (this.attention === 'gemma3') {
-        cfg.rope_theta_swa = 10000.0;
+        cfg.rope_theta_swa = cfg.file_rope_theta_swa || 10000.0;
         cfg.sliding_window = cfg.file_sliding_window || 512;
       }
       this.config = cfg;
@@ -208,4 +238,4 @@ async function createGemmaEngine(options) {
 }
 
 module.exports = { createGemmaEngine: createGemmaEngine, GemmaEngineImpl: GemmaEngineImpl,
-  defaultConfig: defaultConfig };
+  defaultConfig: defaultConfig, MODEL_FILES: MODEL_FILES, resolveModel: resolveModel };

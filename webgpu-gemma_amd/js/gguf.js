@@ -156,6 +156,8 @@ function configFromGGUF(gguf, base, maxContext) {
   if (win !== null) c.file_sliding_window = win;
   const theta = k('rope.freq_base');
   if (theta !== null) c.file_rope_theta = theta;
+  const thetaSwa = k('rope.freq_base_swa');
+  if (thetaSwa !== null) c.file_rope_theta_swa = thetaSwa;
   const tokens = gguf.kv.get('tokenizer.ggml.tokens');
   if (tokens && tokens.type === 'array') c.vocab_size = tokens.value.length;
   c.q_dim = c.num_q_heads * c.head_dim;
