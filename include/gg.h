@@ -217,6 +217,20 @@ int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen_bitmap
                      const gg_sample* s, double u, void* workspace, void* topk_out,
                      int32_t* out_token, void* stream);
 
+/* gg_select_logits without a workspace argument and without any device
+ * allocation: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. The workspace is a static 67,840-byte device array, one
+ * copy per GPU, held until the process ends; its address is looked up once
+ * per device on the first call there. Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other streams or host threads) race.
+ * Returns GG_ERR_INVALID, with a message on stderr, when n would need a
+ * larger workspace than the static one (gg_select_workspace_size(n) bytes;
+ * today that size does not depend on n). Same results as gg_select_logits. */
+int gg_select_logits_noalloc(const float* logits, int32_t n, const uint32_t* seen_bitmap,
+                             const gg_sample* s, double u, void* topk_out, int32_t* out_token,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1354,11 +1355,13 @@ size_t gg_select_workspace_size(int32_t n) {
   return 256 + (size_t)kSelBlocks * 256 * 8 + 512 * 4;
 }
 
-int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s, double u,
-                     void* workspace, void* topk_out, int32_t* out_token, void* stream) {
-  if (!logits || n <= 0 || !s || !workspace || !out_token) return GG_ERR_INVALID;
-  hipStream_t hs = (hipStream_t)stream;
-  char* ws = (char*)workspace;
+}  // extern "C"
+
+// Token selection with the workspace at ws (DevState | cand_val | cand_id |
+// top, gg_select_workspace_size bytes): shared by gg_select_logits and
+// gg_select_logits_noalloc.
+static int select_with_workspace(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s,
+                                 double u, char* ws, void* topk_out, int32_t* out_token, hipStream_t hs) {
   DevState h{};
   h.temperature = s->temperature;
   h.top_p = s->top_p;
@@ -1381,6 +1384,54 @@ int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const
   if (hipStreamSynchronize(hs) != hipSuccess) return GG_ERR_HIP;
   *out_token = back.out_token;
   return GG_OK;
+}
+
+// Workspace of gg_select_logits_noalloc: one copy per device, held until the
+// process ends. Host code never passes `scratch` itself to a kernel or copy
+// (on the host it names a stand-in, not device memory); it uses the device
+// address hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocScratchBytes = 256 + (size_t)kSelBlocks * 256 * 8 + 512 * 4;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device.
+static int scratch_address(char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return GG_ERR_NO_DEVICE;
+  if (dev < 0 || dev >= kMaxScratchDevices) return GG_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return GG_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = (char*)g_scratch_ptr[dev];
+  return GG_OK;
+}
+
+extern "C" {
+
+int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s, double u,
+                     void* workspace, void* topk_out, int32_t* out_token, void* stream) {
+  if (!logits || n <= 0 || !s || !workspace || !out_token) return GG_ERR_INVALID;
+  return select_with_workspace(logits, n, seen, s, u, (char*)workspace, topk_out, out_token, (hipStream_t)stream);
+}
+
+int gg_select_logits_noalloc(const float* logits, int32_t n, const uint32_t* seen, const gg_sample* s, double u,
+                             void* topk_out, int32_t* out_token, void* stream) {
+  if (!logits || n <= 0 || !s || !out_token) return GG_ERR_INVALID;
+  if (gg_select_workspace_size(n) > kNoAllocScratchBytes) {
+    std::fprintf(stderr, "gg_select_logits_noalloc: %d logits need a %zu-byte workspace, above the %zu-byte "
+                 "static one\n", n, gg_select_workspace_size(n), kNoAllocScratchBytes);
+    return GG_ERR_INVALID;
+  }
+  char* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != GG_OK) return rc;
+  return select_with_workspace(logits, n, seen, s, u, ws, topk_out, out_token, (hipStream_t)stream);
 }
 
 }  // extern "C"

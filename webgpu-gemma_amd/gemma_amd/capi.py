@@ -114,6 +114,8 @@ _SIGS = {
     "gg_select_workspace_size": (ctypes.c_size_t, [ctypes.c_int32]),
     "gg_select_logits": (ctypes.c_int, [_P, ctypes.c_int32, _P, ctypes.POINTER(GGSample), ctypes.c_double, _P, _P,
                                         ctypes.POINTER(ctypes.c_int32), _P]),
+    "gg_select_logits_noalloc": (ctypes.c_int, [_P, ctypes.c_int32, _P, ctypes.POINTER(GGSample), ctypes.c_double,
+                                                _P, ctypes.POINTER(ctypes.c_int32), _P]),
 }
 
 
@@ -304,4 +306,14 @@ def select_logits(logits_ptr: int, n: int, seen_ptr: int | None, temperature, to
     s = sample(temperature, top_p, rep_penalty)
     _check(None, lib().gg_select_logits(logits_ptr, n, seen_ptr or None, ctypes.byref(s), float(u), ws_ptr,
                                         topk_ptr or None, ctypes.byref(out), _stream_ptr(stream)))
+    return out.value
+
+
+def select_logits_noalloc(logits_ptr: int, n: int, seen_ptr: int | None, temperature, top_p, rep_penalty, u,
+                          topk_ptr: int | None = None, stream=None) -> int:
+    """select_logits with the library's static per-device workspace (no device allocation)."""
+    out = ctypes.c_int32(-1)
+    s = sample(temperature, top_p, rep_penalty)
+    _check(None, lib().gg_select_logits_noalloc(logits_ptr, n, seen_ptr or None, ctypes.byref(s), float(u),
+                                                topk_ptr or None, ctypes.byref(out), _stream_ptr(stream)))
     return out.value
