@@ -290,7 +290,7 @@ def main():
                 "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic("decode_step_traffic.txt"), "bytes_per_launch": k_bytes,
                 "avg_launch_us": round(k_ms * 1e3, 2), "launches": len(fwd_ms),
-                "timing": "HIP events around each graph launch of the step (state upload node + k_decode) over "
+                "timing": "HIP events around each k_decode launch (the step's inputs are kernel arguments) over "
                           f"{len(fwd_ms)} decode steps"}
     else:
         # dominant-kernel timing: the same forward pass with its kernels

@@ -539,9 +539,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   if (tid == 0) S.fail = 0;
   const DevState* st = a.st;
   const uint32_t epoch = st->epoch;
-  const int pos = st->pos;
-  const int cur = st->cursor;
-  const int token = cur < 0 ? st->token : a.tokens[cur];
+  const bool args_in = MODE == DEC_STEP && a.in_use != 0;
+  const int pos = args_in ? a.in_pos : st->pos;
+  const int cur = args_in ? -1 : st->cursor;
+  const int token = args_in ? a.in_token : cur < 0 ? st->token : a.tokens[cur];
   const uint32_t base = epoch * (uint32_t)(a.L + 2);
   __syncthreads();
 
@@ -836,7 +837,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     a.top[2 * tid] = __float_as_uint(m);
     a.top[2 * tid + 1] = id;
   }
-  const int tok = select_token(S.sel, m, id, tid < 256, st, a.seen, a.V);
+  SampleIn sp = sample_of(st);
+  if (args_in) {
+    sp.temperature = a.in_temperature;
+    sp.top_p = a.in_top_p;
+    sp.rep_penalty = a.in_rep_penalty;
+    sp.u = a.in_u;
+  }
+  const int tok = select_token(S.sel, m, id, tid < 256, sp, a.seen, a.V);
   if (tid == 0) {
     a.st->out_token = tok;
     a.host_out[0] = tok;

@@ -248,15 +248,25 @@ struct SelShared {
 // differences, f64 sums, top-p cutoff and the walk with the draw u. Every
 // thread of the block calls it (it holds block barriers); the token is
 // returned to all threads.
-static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool active, const DevState* st,
-                            const uint32_t* seen, int V) {
+static __device__ SampleIn sample_of(const DevState* st) {
+  SampleIn p;
+  p.temperature = st->temperature;
+  p.top_p = st->top_p;
+  p.rep_penalty = st->rep_penalty;
+  p.u = st->u;
+  p.seen_count = st->seen_count;
+  return p;
+}
+
+static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool active, const SampleIn& p,
+                                   const uint32_t* seen, int V) {
   const int tid = threadIdx.x;
   if (active) {
     sh.tv[tid] = m;
     sh.ti[tid] = id;
   }
   __syncthreads();
-  const double T = st->temperature, rep = st->rep_penalty;
+  const double T = p.temperature, rep = p.rep_penalty;
   if (T == 0.0 && rep <= 1.0) {
     for (int stride = 128; stride > 0; stride >>= 1) {
       if (active && tid < stride && sh.tv[tid + stride] > sh.tv[tid]) {
@@ -272,7 +282,7 @@ static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool act
     cd.val = (double)m;
     cd.ord = tid;
     cd.id = id;
-    if (rep > 1.0 && st->seen_count > 0 && id < (uint32_t)V && ((seen[id >> 5] >> (id & 31)) & 1u)) {
+    if (rep > 1.0 && p.seen_count > 0 && id < (uint32_t)V && ((seen[id >> 5] >> (id & 31)) & 1u)) {
       if (cd.val > 0) cd.val /= rep;
       else cd.val *= rep;
     }
@@ -301,11 +311,11 @@ static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool act
     int cutoff = 256;
     for (int i = 0; i < 256; ++i) {
       cum += (double)sh.probs[i] / sum;
-      if (cum >= st->top_p) { cutoff = i + 1; break; }
+      if (cum >= p.top_p) { cutoff = i + 1; break; }
     }
     double subset = 0.0;
     for (int i = 0; i < cutoff; ++i) subset += (double)sh.probs[i];
-    double r = st->u * subset;
+    double r = p.u * subset;
     int pick = -1;
     for (int i = 0; i < cutoff; ++i) {
       r -= (double)sh.probs[i];

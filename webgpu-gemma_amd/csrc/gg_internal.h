@@ -70,6 +70,16 @@ inline Q8Layout q8_layout(int rows, int K, int force_ci = 0) {
 // Per-step scalars the captured graphs read from device memory.
 // The host rewrites the fields before `seen_count` ahead of every launch;
 // `seen_count` and `out_token` are maintained by the kernels.
+// Sampling inputs of one token selection (engine.ts:862-901 reads them from
+// the generate() options and Math.random()).
+struct SampleIn {
+  double temperature;
+  double top_p;
+  double rep_penalty;
+  double u;
+  int32_t seen_count;
+};
+
 struct DevState {
   int32_t pos;          // position of the token being processed
   int32_t cursor;       // index into the device token array; < 0: embed `token`
@@ -274,6 +284,11 @@ struct DecodeArgs {
   int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag
   long long spin_limit;    // s_memrealtime ticks (100 MHz) one hand-off may wait
   long long* timeline;     // optional [256][L][kDecEvents] s_memrealtime stamps (null: off)
+  // in_use != 0: this launch's position, token and sampling parameters are
+  // these arguments rather than DevState's host-written head, so a decode step
+  // needs no state upload before its launch (DEC_STEP only)
+  int32_t in_use, in_pos, in_token;
+  double in_temperature, in_top_p, in_rep_penalty, in_u;
 };
 constexpr int kDecEvents = 16;  // timeline events per (block, layer)
 int launch_decode(int mode, const DecodeArgs& a, void* stream);

@@ -855,7 +855,7 @@ __global__ __launch_bounds__(256) void k_select2(SelectArgs a, int nb) {
   }
   a.top[2 * tid] = __float_as_uint(m);
   a.top[2 * tid + 1] = id;
-  const int token = select_token(sh, m, id, true, a.st, a.seen, a.V);
+  const int token = select_token(sh, m, id, true, sample_of(a.st), a.seen, a.V);
   if (tid == 0) {
     a.st->out_token = token;
     if (a.host_out) a.host_out[0] = token;

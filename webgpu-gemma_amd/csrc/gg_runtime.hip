@@ -451,14 +451,28 @@ int record_step(gg_ctx* c) {
   return record_select_impl(c, true);
 }
 
-// The same step on the persistent kernel: with a vocabulary that is a
-// multiple of 16384 its LM head and selection run in the same launch.
+// The step on the persistent kernel when its LM head and selection cannot
+// run in the same launch (a vocabulary that is not a multiple of 16384):
+// forward launch, then the selection kernels. Otherwise the whole step is
+// one launch_fused_step.
 int record_fused_step(gg_ctx* c) {
   GG_TRY(push_state(c, 0, offsetof(DevState, seen_count)));
-  if (c->fused_step)
-    return launch_rc(c, launch_decode(DEC_STEP, c->dargs, c->stream), "persistent decode kernel");
   GG_TRY(record_fused_fwd(c));
   return record_select(c);
+}
+
+// A decode step on the persistent kernel (DEC_STEP) whose position, token and
+// sampling parameters are kernel arguments: one launch, no state upload.
+int launch_fused_step(gg_ctx* c) {
+  DecodeArgs a = c->dargs;
+  a.in_use = 1;
+  a.in_pos = c->h_st->pos;
+  a.in_token = c->h_st->token;
+  a.in_temperature = c->h_st->temperature;
+  a.in_top_p = c->h_st->top_p;
+  a.in_rep_penalty = c->h_st->rep_penalty;
+  a.in_u = c->h_st->u;
+  return launch_rc(c, launch_decode(DEC_STEP, a, c->stream), "persistent decode kernel");
 }
 
 int run_forward(gg_ctx* c) {
@@ -1047,7 +1061,7 @@ int gg_finalize(gg_ctx* c) {
     GG_TRY(capture(c, record_step, &c->g_step));
     if (c->fused) {
       GG_TRY(capture(c, record_fused_fwd, &c->g_ffwd));
-      GG_TRY(capture(c, record_fused_step, &c->g_fstep));
+      if (!c->fused_step) GG_TRY(capture(c, record_fused_step, &c->g_fstep));
     }
   }
   c->finalized = true;
@@ -1090,7 +1104,8 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (with_forward && !ev) {
     if (c->fused) {
       GG_TRY(fused_launch_begin(c));
-      if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
+      if (c->fused_step) GG_TRY(launch_fused_step(c));
+      else if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
       else GG_TRY(record_fused_step(c));
     } else {
       if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
@@ -1107,10 +1122,9 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (with_forward && c->fused && c->fused_step) {
     // timed persistent step: the whole token is one launch (forward, LM
     // head and selection), reported as the forward time with select 0
-    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
     GG_TRY(fused_launch_begin(c));
-    if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
-    else GG_TRY(record_fused_step(c));
+    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+    GG_TRY(launch_fused_step(c));
     GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
     GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
     GG_TRY(sync(c, "step"));
