@@ -49,8 +49,11 @@ namespace {
 constexpr int NT = kDecThreads;
 constexpr int NW = kDecThreads / 64;
 constexpr int kEPT = 2048 / NT;     // residual elements per thread (H <= 2048)
-constexpr int kNifGu = (kDecMaxH / 64 + NW - 1) / NW;  // gate/up items per wave (one 64-row group, Kp = H / 64)
-constexpr int kDR = (kDecMaxH + NT - 1) / NT;           // W_down rows per thread
+constexpr int kMaxKq = kDecMaxH / 64;                  // pair columns of a gate/up row (64 k each)
+constexpr int kMaxKh = (kMaxKq + 1) / 2;                // gate/up scale dwords per lane
+constexpr int kDT = (kDecMaxH / 32 + NW - 1) / NW;      // W_down 32-row tiles per wave
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 // Thread / block index as values the compiler cannot hoist out of the layer
 // loop: loop-invariant addresses and offsets derived from them would stay
@@ -176,6 +179,11 @@ __device__ __forceinline__ float red_row(const float (*red)[kDecMaxRows], int t)
 
 struct Smem {
   float4 xs4[kMaxK / 64 * kXPad / 4];   // GEMV input x (K <= 8192)
+  i32x4 xq4[kMaxKq * 12];               // FFN input as int8 planes: [pair column][plane][64]
+  float4 xsc4[2][kMaxKq / 4];           // ... block scales: [block parity][pair column]
+  i32x4 xa4[6];                         // GeGLU output as int8 planes: [plane][32]
+  i32x4 zq;                             // zero A operand of the lanes outside the planes
+  float sact;                           // ... the GeGLU planes' scale
   float res[2048];                      // residual stream (H <= 2048), identical in every block
   float red[NW][kDecMaxRows];
   float shw[2][NW];
@@ -250,6 +258,95 @@ __device__ __forceinline__ void norm_to_xs(Smem& S, const float* r, const float*
     const int e = tid + NT * i;
     if (e < H) xs[xs_index(e)] = (r[i] * w[i]) * ri;
   }
+}
+
+// ---- int8-MFMA FFN ----------------------------------------------------------
+// A 32-element block of an activation vector with max |v| = m is carried as
+// three int8 planes, v = S (p0 + p1 / 254 + p2 / 254^2) with S = m / 127
+// (p0 = rint(v / S), each next plane the rounded remainder times 254): 24
+// bits of the block's range, about the precision of the f32 value. The
+// MFMA's int32 sums of weight x plane are exact; the scales S and the Q8_0
+// block scale apply in f32 afterwards.
+__device__ __forceinline__ void split3(float y, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  const float a = rintf(y);
+  const float r = (y - a) * 254.f;
+  const float bq = rintf(r);
+  const float cq = rintf((r - bq) * 254.f);
+  p0 = (uint32_t)(int)a & 255u;
+  p1 = (uint32_t)(int)bq & 255u;
+  p2 = (uint32_t)(int)cq & 255u;
+}
+__device__ __forceinline__ float planes_value(int c0, int c1, int c2) {
+  return fmaf((float)c2, 1.f / 64516.f, fmaf((float)c1, 1.f / 254.f, (float)c0));
+}
+// Max over the 32 lanes of a half wave.
+__device__ __forceinline__ float half_wave_max(float m) {
+  m = fmaxf(m, dpp_mov<0xB1>(m));
+  m = fmaxf(m, dpp_mov<0x4E>(m));
+  m = fmaxf(m, dpp_mov<0x141>(m));
+  m = fmaxf(m, dpp_mov<0x140>(m));
+  return fmaxf(m, __shfl_xor(m, 16, 64));
+}
+
+// The gate/up GEMV input x (f32 in xs) as int8 planes: four threads per
+// 32-element block, eight elements each, one pass over H / 32 blocks.
+__device__ __forceinline__ void planes_from_xs(Smem& S, int H) {
+  const int tid = tidx();
+  if (tid < H / 8) {
+    const int blk = tid >> 2, sub = tid & 3;
+    const float* xs = (const float*)S.xs4 + xs_index(32 * blk) + 8 * sub;
+    const float4 v0 = *(const float4*)xs, v1 = *(const float4*)(xs + 4);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+    m = fmaxf(m, dpp_mov<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = fmaxf(m, dpp_mov<0x4E>(m));   // quad_perm [2,3,0,1]
+    const float inv = m > 0.f ? 127.f * __builtin_amdgcn_rcpf(m) : 0.f;
+    uint32_t q[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t p0, p1, p2;
+      split3(v[j] * inv, p0, p1, p2);
+      q[0][j >> 2] |= p0 << (8 * (j & 3));
+      q[1][j >> 2] |= p1 << (8 * (j & 3));
+      q[2][j >> 2] |= p2 << (8 * (j & 3));
+    }
+    uint8_t* dst = (uint8_t*)S.xq4 + (blk >> 1) * 192 + (blk & 1) * 32 + 8 * sub;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) *(uint2*)(dst + 64 * pl) = make_uint2(q[pl][0], q[pl][1]);
+    if (sub == 0) ((float*)S.xsc4[blk & 1])[blk >> 1] = m * (1.f / 127.f);
+  }
+}
+
+// Gate/up rows of tile wv (16 rows: gate rows 16 wv .. for wv < 2, up rows
+// 16 (wv - 2) .. otherwise) over the pair columns on v_mfma_i32_16x16x64_i8.
+// A: the input planes, rows 0-2 for block 2c and rows 4-6 for block 2c + 1,
+// each at the k-groups of its block (lane l: row l % 16, k-group l / 16);
+// the other lanes read a zero operand, and so does every lane past Kq (the
+// plane rows of pair columns >= Kq are never written), so the loop has no
+// branch. B: the tile's weights (lane l: weight row l % 16, the same
+// k-group). Result lanes 0-15 / 16-31 hold the three plane sums of block
+// 2c / 2c + 1 for weight row l % 16; returns that lane's f32 sum over all c.
+__device__ __forceinline__ float gate_up_mfma(const Smem& S, const i32x4* wb, const uint32_t* wsc) {
+  const int lane = tidx() & 63, i = lane & 15, g = lane >> 4;
+  const bool valid = (i < 3 && g < 2) || (i >= 4 && i < 7 && g >= 2);
+  const int p = i < 3 ? i : i - 4;
+  const int hb = (lane >> 4) & 1;
+  const uint8_t* ab = valid ? (const uint8_t*)S.xq4 + p * 64 + 16 * g : (const uint8_t*)&S.zq;
+  const int as = valid ? 192 : 0;
+  const float* sc = (const float*)S.xsc4[hb];
+  const i32x4 zero = {0, 0, 0, 0};
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxKq; ++c) {
+    const i32x4 A = *(const i32x4*)(ab + c * as);
+    const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, wb[c], zero, 0, 0, 0);
+    const uint32_t w2 = wsc[c >> 1];
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? w2 >> 16 : w2 & 0xffffu));
+    acc = fmaf(planes_value(C[0], C[1], C[2]), sc[c] * d, acc);
+  }
+  return acc;
 }
 
 // Poll n <= NT * PER LL words into the GEMV input x.
@@ -537,6 +634,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   const int H = a.H;
   const long long lim = a.spin_limit;
   if (tid == 0) S.fail = 0;
+  // plane rows of pair columns >= Kq and their scales stay zero all launch
+  for (int i = tid; i < kMaxKq * 12; i += NT) S.xq4[i] = i32x4{0, 0, 0, 0};
+  if (tid < 2 * kMaxKq / 4) (&S.xsc4[0][0])[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tid == 0) S.zq = i32x4{0, 0, 0, 0};
   const DevState* st = a.st;
   const uint32_t epoch = st->epoch;
   const bool args_in = MODE == DEC_STEP && a.in_use != 0;
@@ -566,24 +667,38 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     // ---- Q: residual stream update in every block; QKV rows in [0, 192) ----
     const bool qb = b < kDecQBlocks;
     const bool ffb = b < a.g_f;                     // this block runs the FFN block b
-    Pair wq[1], wg[kNifGu];
-    uint32_t dq[kDR][8];                            // W_down input block b: 32 int8 of rows tid + NT i
-    uint16_t dsc[kDR];                              // and their f16 scales
+    Pair wq[1];
+    i32x4 wgb[kMaxKq];                              // gate/up tile wv: B operands per pair column
+    uint32_t wgs[kMaxKh];                           // and its block scales (lanes 0-31)
+    i32x4 wdb[kDT];                                 // W_down input block b, 32-row tiles wv + NW k
+    uint16_t wds[kDT];                              // and the f16 scale of row 32 T + lane (lanes 0-31)
     float wn[kEPT];
     // the FFN weights are issued as soon as the block's Q or A work is done:
     // they stream in while attention runs and the O hand-off waits
     auto issue_ffn = [&]() {
       if (!ffb) return;
-      mg_issue<1, kNifGu>(Ly.guf, Kq, Kq, b * Kq, Kq, wg);
-      const GG_GLOBAL uint8_t* col = gmem(Ly.dcb) + (size_t)b * 34 * H;
+      const int lane = tid & 63, wv = tid >> 6;
+      const int Kh = (Kq + 1) / 2, nT = H / 32;
+      const GG_GLOBAL uint8_t* gb =
+          gmem(Ly.guf) + (size_t)b * ((size_t)Kq * 4096 + (size_t)Kh * 512);
 #pragma unroll
-      for (int i = 0; i < kDR; ++i) {
-        const int rr = min(tid + NT * i, H - 1);
-        const GG_GLOBAL u32x4* q4 = (const GG_GLOBAL u32x4*)(col + 2 * H + 32 * rr);
-        const u32x4 q0 = __builtin_nontemporal_load(q4), q1 = __builtin_nontemporal_load(q4 + 1);
-        dq[i][0] = q0.x; dq[i][1] = q0.y; dq[i][2] = q0.z; dq[i][3] = q0.w;
-        dq[i][4] = q1.x; dq[i][5] = q1.y; dq[i][6] = q1.z; dq[i][7] = q1.w;
-        dsc[i] = ((const GG_GLOBAL uint16_t*)col)[rr];
+      for (int c = 0; c < kMaxKq; ++c)
+        wgb[c] = __builtin_nontemporal_load(
+            (const GG_GLOBAL i32x4*)(gb + (size_t)min(c, Kq - 1) * 4096 + wv * 1024 + lane * 16));
+#pragma unroll
+      for (int m = 0; m < kMaxKh; ++m)
+        wgs[m] = __builtin_nontemporal_load(
+            (const GG_GLOBAL uint32_t*)(gb + (size_t)Kq * 4096 + ((size_t)(wv * Kh + min(m, Kh - 1)) * 32 + (lane & 31)) * 4));
+      const GG_GLOBAL uint8_t* col = gmem(Ly.dcb) + (size_t)b * 34 * H;
+      // tile T as the B operand of v_mfma_i32_16x16x64_i8: lane l holds row
+      // 32 T + 16 (l / 32) + l % 16, input bytes 16 ((l / 16) & 1) .. +15
+#pragma unroll
+      for (int k = 0; k < kDT; ++k) {
+        const int t0 = 32 * min(wv + NW * k, nT - 1);
+        const int rb = t0 + 16 * (lane >> 5) + (lane & 15);
+        wdb[k] = __builtin_nontemporal_load(
+            (const GG_GLOBAL i32x4*)(col + 2 * H + 32 * rb + 16 * ((lane >> 4) & 1)));
+        wds[k] = ((const GG_GLOBAL uint16_t*)col)[t0 + (lane & 31)];
       }
     };
     if (qb) mg_issue<8, 1>(Ly.qkv, Kq, a.kps_qkv, b * a.kps_qkv, a.kps_qkv, wq);
@@ -640,9 +755,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
 
     // ---- F: post-attention norm + residual + ffn_norm, then in block b < I / 32
     // the gate/up rows of act[32 b .. 32 b + 31] (GeGLU) and that act slice
-    // times W_down's 32-wide input block b: a partial down output ----
+    // times W_down's 32-wide input block b: a partial down output. Both
+    // products run on the int8 MFMA with the activations as int8 planes ----
     {
-      zero_red(S.red);
       float ov[kEPT], wpa[kEPT], wffn[kEPT];
       load_norm(norm_of(a, Ly, 4), H, wpa);
       load_norm(norm_of(a, Ly, 1), H, wffn);
@@ -650,28 +765,53 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 5);
       resid_update(S, ov, wpa, H, a.eps, r, 0);
-      norm_to_xs(S, r, wffn, H, a.eps, 1);
-      __syncthreads();
-      stamp(a, b, l, 9);
       if (ffb) {
-        mg_dots<1, kNifGu>(wg, (const float*)S.xs4, Kq, Kq, b, b * Kq, Kq, S.red);
+        const int lane = tid & 63, wv = tid >> 6;
+        norm_to_xs(S, r, wffn, H, a.eps, 1);
+        __syncthreads();
+        planes_from_xs(S, H);
+        __syncthreads();
+        stamp(a, b, l, 9);
+        float g = gate_up_mfma(S, wgb, wgs);
+        g += __shfl_xor(g, 16, 64);
+        if (lane < 16) S.red[0][16 * wv + lane] = g;
         __syncthreads();
         stamp(a, b, l, 10);
         // gate rows 0..31 of the group, the matching up rows 32..63
-        if (tid < 32) S.act[tid] = gelu_mul(red_row(S.red, tid), red_row(S.red, tid + 32));
+        if (tid < 32) {
+          const float v = gelu_mul(S.red[0][tid], S.red[0][32 + tid]);
+          const float m = half_wave_max(fabsf(v));
+          const float inv = m > 0.f ? 127.f * __builtin_amdgcn_rcpf(m) : 0.f;
+          uint32_t p0, p1, p2;
+          split3(v * inv, p0, p1, p2);
+          uint8_t* xa = (uint8_t*)S.xa4;
+          xa[tid] = (uint8_t)p0;
+          xa[32 + tid] = (uint8_t)p1;
+          xa[64 + tid] = (uint8_t)p2;
+          if (tid == 0) S.sact = m * (1.f / 127.f);
+        }
         __syncthreads();
-        // partial down output of this input block: (sum_k q[r][k] act[k]) * d_r
-        float act[32];
+        // partial down output of this input block on v_mfma_i32_16x16x64_i8,
+        // two 16-row halves of a 32-row tile per product: A rows 0-2 are the
+        // act planes at k-groups 0-1 (the first half's rows in B), rows 4-6
+        // the same planes at k-groups 2-3 (the second half's rows); result
+        // lanes 0-31 hold the three plane sums of row 32 T + lane
+        const int pi = lane & 15, pg = lane >> 4;
+        const bool av = (pi < 3 && pg < 2) || (pi >= 4 && pi < 7 && pg >= 2);
+        const i32x4 A = *(const i32x4*)(av ? (const uint8_t*)S.xa4 + 32 * (pi & 3) + 16 * (pg & 1)
+                                           : (const uint8_t*)&S.zq);
+        const float sact = S.sact;
+        const i32x4 zero = {0, 0, 0, 0};
+        float y[kDT];
 #pragma unroll
-        for (int k = 0; k < 32; ++k) act[k] = S.act[k];
+        for (int k = 0; k < kDT; ++k) {
+          const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, wdb[k], zero, 0, 0, 0);
+          y[k] = (planes_value(C[0], C[1], C[2]) * sact) * (float)__builtin_bit_cast(_Float16, wds[k]);
+        }
 #pragma unroll
-        for (int i = 0; i < kDR; ++i) {
-          const int rr = tid + NT * i;
-          float sacc = 0.f;
-#pragma unroll
-          for (int k = 0; k < 32; ++k) sacc = fmaf(sbyte(dq[i][k >> 2], k & 3), act[k], sacc);
-          const float y = sacc * (float)__builtin_bit_cast(_Float16, dsc[i]);
-          if (rr < H) ll_st(a.x_dpart + (size_t)b * H + rr, y, tag);
+        for (int k = 0; k < kDT; ++k) {
+          const int T = wv + NW * k;
+          if (lane < 32 && T < H / 32) ll_st(a.x_dpart + (size_t)b * H + 32 * T + lane, y[k], tag);
         }
         stamp(a, b, l, 6);
       }

@@ -316,6 +316,11 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream);
 int launch_embed_row(const uint8_t* embd, int kps, float scale, int token, int H, float* out, void* stream);
 // GGUF Q8_0 rows -> column-block layout (per 32-wide block: f16 scales [rows], int8 [rows][32]).
 int launch_repack_colblock(const uint8_t* src, uint8_t* dst, long long rows, int K, void* stream);
+// Gate/up copy of the persistent decode kernel in the int8-MFMA tile layout
+// (bytes per 32-row pair of gate and up rows: gum_group_bytes(K)); up = 0
+// writes the gate tiles, up = 1 the up tiles.
+__host__ __device__ inline size_t gum_group_bytes(int K) { return (size_t)(K / 64) * 4096 + (size_t)((K / 64 + 1) / 2) * 512; }
+int launch_repack_gum(const uint8_t* src, uint8_t* dst, long long rows, int K, int up, void* stream);
 // Class-major copy of the CI = 1 LM head (rows a multiple of 16384).
 int launch_class_major(const uint8_t* src, uint8_t* dst, long long rows, int Kp, void* stream);
 // GGUF Q8_0 rows -> prefill GEMM weights: source row r to row r + off, or

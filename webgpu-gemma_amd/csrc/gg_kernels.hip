@@ -1504,6 +1504,57 @@ __global__ __launch_bounds__(256) void k_repack_colblock(const uint8_t* __restri
   for (int i = 0; i < 32; ++i) q[i] = blk[2 + i];
 }
 
+// Gate/up copy of the persistent decode kernel laid out as the B operands of
+// v_mfma_i32_16x16x64_i8. Group g holds gate rows 32g .. 32g + 31 and up rows
+// 32g .. 32g + 31 as four 16-row tiles t (0, 1: gate; 2, 3: up). For pair
+// column c (k in [64c, 64c + 64)) tile t is 1 KB at c * 4096 + t * 1024, where
+// lane l's 16 bytes are row 16 (t & 1) + l % 16 of its half at k = 64c +
+// 16 (l / 16) .. +15. After the Kp * 4096 int8 bytes come the block scales,
+// [t][m][lane < 32] dwords: the f16 scales of pair columns 2m (low half) and
+// 2m + 1 (high half) for row 16 (t & 1) + lane % 16, Q8_0 block 2c + lane / 16.
+// One thread per 16-byte chunk, then one per scale dword, of the gate (up = 0)
+// or up (up = 1) half.
+__global__ __launch_bounds__(256) void k_repack_gum(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                    long long rows, int K, int up) {
+  const int Kp = K / 64, Kh = (Kp + 1) / 2;
+  const size_t gbytes = gum_group_bytes(K), rowb = (size_t)K / 32 * 34;
+  const long long groups = rows / 32;
+  const long long nch = groups * Kp * 2 * 64, nsc = groups * 2 * Kh * 32;
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < nch) {
+    const int lane = (int)(i % 64);
+    long long q = i / 64;
+    const int th = (int)(q % 2);
+    q /= 2;
+    const int c = (int)(q % Kp);
+    const long long g = q / Kp;
+    const long long row = 32 * g + 16 * th + lane % 16;
+    const int k0 = 64 * c + 16 * (lane / 16);
+    const uint8_t* sp = src + row * rowb + (size_t)(k0 / 32) * 34 + 2 + k0 % 32;
+    uint8_t* dp = dst + g * gbytes + (size_t)c * 4096 + (size_t)(th + 2 * up) * 1024 + (size_t)lane * 16;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dp[j] = sp[j];
+  } else if (i < nch + nsc) {
+    long long q = i - nch;
+    const int lane = (int)(q % 32);
+    q /= 32;
+    const int m = (int)(q % Kh);
+    q /= Kh;
+    const int th = (int)(q % 2);
+    const long long g = q / 2;
+    const long long row = 32 * g + 16 * th + lane % 16;
+    uint32_t v = 0;
+    for (int h = 0; h < 2; ++h) {
+      const int c = 2 * m + h;
+      if (c < Kp) {
+        const uint8_t* bp = src + row * rowb + (size_t)(2 * c + lane / 16) * 34;
+        v |= (uint32_t)(bp[0] | (bp[1] << 8)) << (16 * h);
+      }
+    }
+    *(uint32_t*)(dst + g * gbytes + (size_t)Kp * 4096 + ((size_t)((th + 2 * up) * Kh + m) * 32 + lane) * 4) = v;
+  }
+}
+
 // Embedding row of one token through embed_value (parity reads).
 __global__ __launch_bounds__(256) void k_embed_row(const uint8_t* embd, int kps, float scale, int token, int H,
                                                    float* out) {
@@ -1719,6 +1770,15 @@ int launch_repack(const uint8_t* src, uint8_t* dst, const Q8Layout& L, long long
 
 int launch_embed_row(const uint8_t* embd, int kps, float scale, int token, int H, float* out, void* stream) {
   hipLaunchKernelGGL(k_embed_row, dim3(1), dim3(256), 0, (hipStream_t)stream, embd, kps, scale, token, H, out);
+  return (int)hipGetLastError();
+}
+
+int launch_repack_gum(const uint8_t* src, uint8_t* dst, long long rows, int K, int up, void* stream) {
+  if (rows <= 0 || rows % 32 || K <= 0 || K % 64) return (int)hipErrorInvalidValue;
+  const int Kp = K / 64, Kh = (Kp + 1) / 2;
+  const long long total = rows / 32 * (Kp * 2 * 64 + 2 * Kh * 32);
+  hipLaunchKernelGGL(k_repack_gum, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, src,
+                     dst, rows, K, up);
   return (int)hipGetLastError();
 }
 

@@ -97,9 +97,8 @@ struct gg_ctx {
   float *s_kc = nullptr, *s_vc = nullptr;   // [L][ctx][256]
   // the persistent kernel's FFN copies: gate/up in 64-row groups (32 gate +
   // the 32 matching up rows, CI = 1) and down in 32-wide column blocks
-  Q8Layout lay_guf{};
   uint8_t *s_guf = nullptr, *s_dcb = nullptr;
-  size_t st_dcb = 0;
+  size_t st_guf = 0, st_dcb = 0;
 
   // work buffers
   float *qkv_out = nullptr, *attn_part = nullptr, *attn_out = nullptr, *o_out = nullptr;
@@ -718,9 +717,9 @@ gg_ctx* gg_create(const gg_config* cfg) {
   // FFN copies of the persistent decode kernel, where its limits allow it
   if (c->NQ == kAttnMaxQ && c->CTX <= kDecMaxCtx && c->H <= kDecMaxH && c->I % 32 == 0 &&
       c->I / 32 <= kDecMaxFBlocks) {
-    c->lay_guf = q8_layout(2 * c->I, c->H, 1);
+    c->st_guf = (size_t)(c->I / 32) * gum_group_bytes(c->H);
     c->st_dcb = (size_t)(c->I / 32) * 34 * c->H;
-    if (dalloc(c, &c->s_guf, c->L * c->lay_guf.bytes()) || dalloc(c, &c->s_dcb, c->L * c->st_dcb)) return fail(0);
+    if (dalloc(c, &c->s_guf, c->L * c->st_guf) || dalloc(c, &c->s_dcb, c->L * c->st_dcb)) return fail(0);
   }
   for (int l = 0; l < c->L; ++l) {
     Layer& Ly = c->layers[l];
@@ -835,8 +834,8 @@ int gg_upload_tensor(gg_ctx* c, const char* name, uint32_t type, const uint64_t*
   GG_TRY(launch_rc(c, launch_repack(c->staging, dst, *lay, rows, off, half, c->stream), "repack"));
   if (layer >= 0 && c->s_guf) {
     if (bit == Q_GATE || bit == Q_UP)
-      GG_TRY(launch_rc(c, launch_repack(c->staging, c->s_guf + layer * c->lay_guf.bytes(), c->lay_guf, rows,
-                                        bit == Q_UP ? 32 : 0, 32, c->stream), "repack"));
+      GG_TRY(launch_rc(c, launch_repack_gum(c->staging, c->s_guf + layer * c->st_guf, rows, (int)K,
+                                            bit == Q_UP ? 1 : 0, c->stream), "repack"));
     if (bit == Q_DOWN)
       GG_TRY(launch_rc(c, launch_repack_colblock(c->staging, c->s_dcb + layer * c->st_dcb, rows, (int)K, c->stream),
                        "repack"));
@@ -994,7 +993,7 @@ int gg_finalize(gg_ctx* c) {
     d.w_dcb = c->s_dcb;
     d.st_qkv = c->lay_qkv.bytes();
     d.st_o = c->lay_o.bytes();
-    d.st_guf = c->lay_guf.bytes();
+    d.st_guf = c->st_guf;
     d.st_dcb = c->st_dcb;
     d.norms = c->s_norm;
     d.norm_stride = c->norm_stride;
