@@ -48,7 +48,7 @@ namespace {
 
 constexpr int NT = kDecThreads;
 constexpr int NW = kDecThreads / 64;
-constexpr int kEPT = 2048 / NT;     // residual elements per thread (H <= 2048)
+constexpr int kEPT = (kDecMaxH + NT - 1) / NT;   // residual elements per thread (H <= kDecMaxH)
 constexpr int kMaxKq = kDecMaxH / 64;                  // pair columns of a gate/up row (64 k each)
 constexpr int kMaxKh = (kMaxKq + 1) / 2;                // gate/up scale dwords per lane
 constexpr int kDT = (kDecMaxH / 32 + NW - 1) / NW;      // W_down 32-row tiles per wave
@@ -90,9 +90,9 @@ __device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag
     uint64_t w[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) w[k] = ll_ld((const uint64_t*)(sb + (uint32_t)(8 * (tid + NT * k))));
-    bool ok = true;
+    bool ok = true;   // no short circuit: one compare per word, no branches
 #pragma unroll
-    for (int k = 0; k < PER; ++k) ok = ok && (tid + NT * k >= n || ll_ok(w[k], tag));
+    for (int k = 0; k < PER; ++k) ok &= (tid + NT * k >= n) | ll_ok(w[k], tag);
     if (ok) {
 #pragma unroll
       for (int k = 0; k < PER; ++k) v[k] = ll_val(w[k]);
@@ -184,7 +184,7 @@ struct Smem {
   i32x4 xa4[6];                         // GeGLU output as int8 planes: [plane][32]
   i32x4 zq;                             // zero A operand of the lanes outside the planes
   float sact;                           // ... the GeGLU planes' scale
-  float res[2048];                      // residual stream (H <= 2048), identical in every block
+  float res[kEPT * NT];                 // residual stream (H <= kDecMaxH), identical in every block
   float red[NW][kDecMaxRows];
   float shw[2][NW];
   int fail;
@@ -455,7 +455,7 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
       for (int i = 0; i < 4; ++i) w[i] = ll_ld(src + (wv == 2 ? 4 * lane + i : lane + 64 * i));
       bool good = true;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) good = good && ll_ok(w[i], tag);
+      for (int i = 0; i < 4; ++i) good &= ll_ok(w[i], tag);
       if (good) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) hx[i] = ll_val(w[i]);
@@ -593,9 +593,9 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
       for (int c = 0; c < kDecChunks; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
       const int si = min(tid, 2 * kDecChunks - 1);   // (m, l) word of threads < 32
       const uint64_t ws = ll_ld(base + (si >> 1) * kDecPart + kHeadDim + (si & 1));
-      bool good = tid >= 2 * kDecChunks || ll_ok(ws, tag);
+      bool good = (tid >= 2 * kDecChunks) | ll_ok(ws, tag);
 #pragma unroll
-      for (int c = 0; c < kDecChunks; ++c) good = good && ll_ok(wo[c], tag);
+      for (int c = 0; c < kDecChunks; ++c) good &= ll_ok(wo[c], tag);
       if (good) {
 #pragma unroll
         for (int c = 0; c < kDecChunks; ++c) oc[c] = ll_val(wo[c]);
@@ -833,7 +833,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + RT * k, a.g_f - 1) * H);
         bool good = true;
 #pragma unroll
-        for (int k = 0; k < PR; ++k) good = good && (mt + RT * k >= a.g_f || ll_ok(w[k], tag));
+        for (int k = 0; k < PR; ++k) good &= (mt + RT * k >= a.g_f) | ll_ok(w[k], tag);
         if (good) {
 #pragma unroll
           for (int k = 0; k < PR; ++k)
@@ -964,7 +964,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
       const uint64_t wv0 = ll_ld(a.x_cand + 2 * tid), wi0 = ll_ld(a.x_cand + 2 * tid + 1);
-      if (ll_ok(wv0, tagC) && ll_ok(wi0, tagC)) {
+      if (ll_ok(wv0, tagC) & ll_ok(wi0, tagC)) {
         m = ll_val(wv0);
         id = __float_as_uint(ll_val(wi0));
         break;
