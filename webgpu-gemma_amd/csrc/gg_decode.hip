@@ -819,10 +819,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
 
     // ---- R: down output rows 8 b .. 8 b + 7 = sum over the I / 32 partials ----
     if (b < a.g_down) {
-      // thread t: row j = t / RT, partials m = t % RT + RT k, summed in
-      // increasing m, then a fixed-order reduction over the row's RT threads
-      constexpr int RT = NT / 8, PR = (kDecMaxFBlocks + RT - 1) / RT;
-      const int j = tid / RT, mt = tid % RT;
+      // thread t: row j = t % 8, partials m = t / 8 + 32 k, so eight
+      // consecutive lanes read the eight rows of one partial (one 64-byte
+      // line); each thread sums its partials in increasing m, then a fixed
+      // xor tree over the wave's m slots and the four waves in order
+      constexpr int PR = (kDecMaxFBlocks + 31) / 32;
+      const int j = tid & 7, mt = tid >> 3;
       const uint64_t* src = a.x_dpart + 8 * b + j;
       const long long t0 = __builtin_amdgcn_s_memrealtime();
       float acc = 0.f;
@@ -830,23 +832,31 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       for (;;) {
         uint64_t w[PR];
 #pragma unroll
-        for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + RT * k, a.g_f - 1) * H);
+        for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + 32 * k, a.g_f - 1) * H);
         bool good = true;
 #pragma unroll
-        for (int k = 0; k < PR; ++k) good &= (mt + RT * k >= a.g_f) | ll_ok(w[k], tag);
+        for (int k = 0; k < PR; ++k) good &= (mt + 32 * k >= a.g_f) | ll_ok(w[k], tag);
         if (good) {
 #pragma unroll
           for (int k = 0; k < PR; ++k)
-            if (mt + RT * k < a.g_f) acc += ll_val(w[k]);
+            if (mt + 32 * k < a.g_f) acc += ll_val(w[k]);
           break;
         }
         if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
       }
       if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 7);
+      acc += __shfl_xor(acc, 8, 64);
+      acc += __shfl_xor(acc, 16, 64);
+      acc += __shfl_xor(acc, 32, 64);
+      if ((tid & 63) < 8) S.red[tid >> 6][j] = acc;
+      __syncthreads();
+      if (tid < 8) {
+        float sum = 0.f;
 #pragma unroll
-      for (int m = 1; m < RT; m <<= 1) acc += __shfl_xor(acc, m, 64);
-      if (mt == 0) ll_st(a.x_down + 8 * b + j, acc, tag);
+        for (int w = 0; w < NW; ++w) sum += S.red[w][tid];
+        ll_st(a.x_down + 8 * b + tid, sum, tag);
+      }
       stamp(a, b, l, 11);
     }
     __syncthreads();
