@@ -396,12 +396,12 @@ __device__ __forceinline__ const float* norm_of(const DecodeArgs& a, const Layer
 }
 
 __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, const LayerView& Ly, int l, int c,
-                                                int h, int pos, uint32_t tag) {
+                                                int h, int pos, uint32_t tag, int nchunks) {
   const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
   const long long lim = a.spin_limit;
   int t_lo, ch, nch;
-  dec_span(pos, Ly.window, kDecChunks, &t_lo, &ch, &nch);
-  uint64_t* part = a.x_part + (size_t)(h * kDecChunks + c) * kDecPart;
+  dec_span(pos, Ly.window, nchunks, &t_lo, &ch, &nch);
+  uint64_t* part = a.x_part + (size_t)(h * kDecChunksG + c) * kDecPart;
   if (c >= nch) {   // past the span: an empty partial (m = -inf)
     for (int d = tid; d < kDecPart; d += NT) ll_st(part + d, d == kHeadDim ? -INFINITY : 0.f, tag);
     return true;
@@ -576,30 +576,31 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
   return true;
 }
 
-// Chunk 0's block of head h: merge the head's 16 chunk partials,
+// Chunk 0's block of head h: merge the head's NC chunk partials,
 // o = sum_c f_c o_c / sum_c f_c l_c with f_c = 2^(m_c - max m) (maxima in
 // log2 units; empty chunks have m_c = -inf), into the O GEMV's input.
-// Threads 0..31 poll the (m, l) words, threads 0..255 one dim of each o_c.
+// Threads 0..2 NC - 1 poll the (m, l) words, threads 0..255 one dim of each o_c.
+template <int NC>
 __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, int h, uint32_t tag) {
   const int tid = tidx();
-  const uint64_t* base = a.x_part + (size_t)h * kDecChunks * kDecPart;
+  const uint64_t* base = a.x_part + (size_t)h * kDecChunksG * kDecPart;
   bool ok = true;
-  float oc[kDecChunks];
+  float oc[NC];
   if (tid < kHeadDim) {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
-      uint64_t wo[kDecChunks];
+      uint64_t wo[NC];
 #pragma unroll
-      for (int c = 0; c < kDecChunks; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
-      const int si = min(tid, 2 * kDecChunks - 1);   // (m, l) word of threads < 32
+      for (int c = 0; c < NC; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
+      const int si = min(tid, 2 * NC - 1);   // (m, l) word of threads < 2 NC
       const uint64_t ws = ll_ld(base + (si >> 1) * kDecPart + kHeadDim + (si & 1));
-      bool good = (tid >= 2 * kDecChunks) | ll_ok(ws, tag);
+      bool good = (tid >= 2 * NC) | ll_ok(ws, tag);
 #pragma unroll
-      for (int c = 0; c < kDecChunks; ++c) good &= ll_ok(wo[c], tag);
+      for (int c = 0; c < NC; ++c) good &= ll_ok(wo[c], tag);
       if (good) {
 #pragma unroll
-        for (int c = 0; c < kDecChunks; ++c) oc[c] = ll_val(wo[c]);
-        if (tid < 2 * kDecChunks) S.red[0][tid] = ll_val(ws);
+        for (int c = 0; c < NC; ++c) oc[c] = ll_val(wo[c]);
+        if (tid < 2 * NC) S.red[0][tid] = ll_val(ws);
         break;
       }
       if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_limit) { ok = false; break; }
@@ -610,10 +611,10 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
   if (tid < kHeadDim) {
     float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < kDecChunks; ++c) M = fmaxf(M, S.red[0][2 * c]);
+    for (int c = 0; c < NC; ++c) M = fmaxf(M, S.red[0][2 * c]);
     float L = 0.f, acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < kDecChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const float f = __builtin_amdgcn_exp2f(S.red[0][2 * c] - M);
       L = fmaf(f, S.red[0][2 * c + 1], L);
       acc = fmaf(f, oc[c], acc);
@@ -725,15 +726,27 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       __syncthreads();
       if (tid < 8) ll_st(a.x_qkv + 8 * b + tid, red_row(S.red, tid), tag);
       stamp(a, b, l, 2);
+      // full-attention layers: blocks [0, 64) also take chunks 16..31
+      if (Ly.window == 0 && b < 64) {
+        const int c = 16 + (b & 7) + 8 * (b >> 5), h = (b >> 3) & 3;
+        if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a); return; }
+      }
       issue_ffn();
     } else {
-      // ---- A: attention (blocks [192, 256)) ----
+      // ---- A: attention (blocks [192, 256): chunks 0..15 of each head) ----
       const int ab = b - kDecQBlocks;
       const int c = (ab & 7) + 8 * (ab >> 5), h = (ab >> 3) & 3;
-      if (!attention_block(a, S, Ly, l, c, h, pos, tag)) { report_timeout(a); return; }
+      const bool glob = Ly.window == 0;
+      if (!attention_block(a, S, Ly, l, c, h, pos, tag, glob ? kDecChunksG : kDecChunks)) {
+        report_timeout(a);
+        return;
+      }
       stamp(a, b, l, 2);
-      if (c == 0 && !merge_head(a, S, l, h, tag)) { report_timeout(a); return; }
-      if (c == 0) stamp(a, b, l, 3);
+      if (c == 0) {
+        const bool mok = glob ? merge_head<kDecChunksG>(a, S, l, h, tag) : merge_head<kDecChunks>(a, S, l, h, tag);
+        if (!mok) { report_timeout(a); return; }
+        stamp(a, b, l, 3);
+      }
       issue_ffn();
     }
     __syncthreads();

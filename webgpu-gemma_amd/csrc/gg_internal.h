@@ -228,7 +228,8 @@ struct SelectArgs {
 constexpr int kDecBlocks = 256;      // blocks of the persistent decode kernel
 constexpr int kDecThreads = 256;     // threads per block (4 waves, one per SIMD: 512 registers each)
 constexpr int kDecQBlocks = 192;     // QKV phase: blocks [0, 192), one 8-row group each (1536 rows)
-constexpr int kDecChunks = 16;       // attention chunks per head: blocks [192, 256) = 16 chunks x 4 heads
+constexpr int kDecChunks = 16;       // attention chunks per head, sliding-window layers: blocks [192, 256)
+constexpr int kDecChunksG = 32;      // ... full-attention layers: blocks [192, 256) and [0, 64)
 constexpr int kDecPart = kHeadDim + 2;   // LL words of one chunk partial: o[256], m, l
 constexpr int kDecMaxRows = 128;     // rows of one phase a block may own
 constexpr int kDecMaxH = 1280;       // hidden sizes of the persistent kernel (its W_down rows per thread)
@@ -266,7 +267,7 @@ struct DecodeArgs {
   const int32_t* tokens;
   // hand-off buffers (LL words)
   uint64_t* x_qkv;         // [NQKV]
-  uint64_t* x_part;        // [4][kDecChunks][kDecPart]
+  uint64_t* x_part;        // [4][kDecChunksG][kDecPart]
   uint64_t* x_attn;        // [QD]
   uint64_t* x_o;           // [H]
   uint64_t* x_dpart;       // [g_f][H] partial down outputs

@@ -974,7 +974,7 @@ int gg_finalize(gg_ctx* c) {
   if (c->fused) {
     DecodeArgs& d = c->dargs;
     // hand-off words; polled buffers hold kDecThreads * (words per thread)
-    const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunks * kDecPart;
+    const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunksG * kDecPart;
     const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = 2048, w_dpart = (size_t)(c->I / 32) * c->H;
     const size_t w_cand = 512;
     c->xll_words = w_qkv + w_part + w_attn + 2 * w_h + w_dpart + w_cand;
