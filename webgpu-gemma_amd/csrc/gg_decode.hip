@@ -878,6 +878,27 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   // ---- end of the pass: post-FFN norm + residual, output norm ----
   const uint32_t tagL = base + (uint32_t)a.L;   // the last layer's down output
   if (MODE == DEC_FWD && b != 0) return;
+  // ---- LM head (DEC_STEP), vocabulary class b: rows b + 256 k, class-major
+  // copy. Wave w takes the class's 64-row groups j = w + 4 q; lane = row, so
+  // each lane runs a whole row's dot product over its Kp items, streamed
+  // with kLmDepth items in flight per wave. The first kLmDepth items are
+  // issued here, before the last hand-off: the weights do not depend on it.
+  const int lane = tid & 63, wv = tid >> 6;
+  const int R = a.V / 256, R64 = R / 64;   // rows and 64-row groups per class
+  const int Kp = H / 64;
+  const int ngw = (R64 - wv + NW - 1) / NW;
+  const int nit = ngw * Kp;
+  auto item_ptr = [&](int i) {   // clamped into the class (a wave without groups loads its last one)
+    const int q = i / Kp, cc = i - q * Kp;
+    const int P = b * R64 + min(wv + NW * q, R64 - 1);
+    return a.lm + ((size_t)P * Kp + cc) * kColBytes;
+  };
+  constexpr int kLmDepth = 6;
+  Pair p[kLmDepth];
+  if (MODE == DEC_STEP) {
+#pragma unroll
+    for (int d = 0; d < kLmDepth; ++d) load_planes(item_ptr(max(min(d, nit - 1), 0)), lane, p[d]);
+  }
   {
     float dv[kEPT], wpost[kEPT], wout[kEPT];
     load_norm(norm_of(a, layer_view(a, a.L - 1), 5), H, wpost);
@@ -910,31 +931,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   }
 
   stamp(a, b, a.L - 1, 14);
-  // ---- LM head, vocabulary class b: rows b + 256 k, class-major copy ----
-  // Wave w takes the class's 64-row groups j = w + 4 q (q < kLmQ); lane =
-  // row, so each lane runs a whole row's dot product over its Kp items,
-  // streamed with kLmDepth items in flight per wave.
-  const int lane = tid & 63, wv = tid >> 6;
-  const int R = a.V / 256, R64 = R / 64;   // rows and 64-row groups per class
-  const int Kp = H / 64;
-  const int ngw = (R64 - wv + NW - 1) / NW;
-  const int nit = ngw * Kp;
-  auto item_ptr = [&](int i) {
-    const int q = i / Kp, cc = i - q * Kp;
-    const int P = b * R64 + wv + NW * q;
-    return a.lm + ((size_t)P * Kp + cc) * kColBytes;
-  };
   const float* xs = (const float*)S.xs4;
-  constexpr int kLmDepth = 6;
   // the class candidate: the first index of the maximum above -1e30, else
   // (-1e30, 0) (strict >, shaders.ts:337-347); this lane's rows come in
   // increasing index order (group q = 0, 1, ...)
   float bv = -1e30f;
   uint32_t bi = 0;
   if (nit > 0) {
-    Pair p[kLmDepth];
-#pragma unroll
-    for (int d = 0; d < kLmDepth; ++d) load_planes(item_ptr(min(d, nit - 1)), lane, p[d]);
     float acc = 0.f;
     int q = 0, cc = 0;
     for (int i = 0; i < nit; i += kLmDepth) {
@@ -980,6 +983,15 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   if (b != 0) return;
 
   // ---- block 0: topk256 and the selection ----
+  // the sampling inputs are read before the candidate poll, so their
+  // latency overlaps it
+  SampleIn sp = sample_of(st);
+  if (args_in) {
+    sp.temperature = a.in_temperature;
+    sp.top_p = a.in_top_p;
+    sp.rep_penalty = a.in_rep_penalty;
+    sp.u = a.in_u;
+  }
   float m = -1e30f;
   uint32_t id = 0;
   bool ok = true;
@@ -1000,20 +1012,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     a.top[2 * tid] = __float_as_uint(m);
     a.top[2 * tid + 1] = id;
   }
-  SampleIn sp = sample_of(st);
-  if (args_in) {
-    sp.temperature = a.in_temperature;
-    sp.top_p = a.in_top_p;
-    sp.rep_penalty = a.in_rep_penalty;
-    sp.u = a.in_u;
-  }
   const int tok = select_token(S.sel, m, id, tid < 256, sp, a.seen, a.V);
   if (tid == 0) {
     a.st->out_token = tok;
     a.host_out[0] = tok;
     if (tok >= 0 && tok < a.V) {
-      a.seen[tok >> 5] |= 1u << (tok & 31);
-      a.st->seen_count += 1;
+      // no-return atomic OR: no load round trip at the end of the launch
+      __hip_atomic_fetch_or(a.seen + (tok >> 5), 1u << (tok & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.st->seen_count = sp.seen_count + 1;
     }
     a.st->pos = pos + 1;
     a.st->cursor = cur + 1;

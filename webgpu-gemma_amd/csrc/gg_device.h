@@ -268,14 +268,26 @@ static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool act
   __syncthreads();
   const double T = p.temperature, rep = p.rep_penalty;
   if (T == 0.0 && rep <= 1.0) {
-    for (int stride = 128; stride > 0; stride >>= 1) {
-      if (active && tid < stride && sh.tv[tid + stride] > sh.tv[tid]) {
-        sh.tv[tid] = sh.tv[tid + stride];
-        sh.ti[tid] = sh.ti[tid + stride];
+    // the tree of strides 128, 64, ..., 1 where slot t takes slot t + s when
+    // that value is strictly greater: the two widest levels from LDS, the
+    // rest in wave 0 (one barrier instead of eight, same comparisons)
+    if (tid < 64) {
+      float v0 = sh.tv[tid], v1 = sh.tv[tid + 64];
+      uint32_t i0 = sh.ti[tid], i1 = sh.ti[tid + 64];
+      const float v2 = sh.tv[tid + 128], v3 = sh.tv[tid + 192];
+      if (v2 > v0) { v0 = v2; i0 = sh.ti[tid + 128]; }
+      if (v3 > v1) { v1 = v3; i1 = sh.ti[tid + 192]; }
+      if (v1 > v0) { v0 = v1; i0 = i1; }
+#pragma unroll
+      for (int s = 32; s > 0; s >>= 1) {
+        const float o = __shfl_down(v0, s, 64);
+        const uint32_t oi = (uint32_t)__shfl_down((int)i0, s, 64);
+        if (tid < s && o > v0) { v0 = o; i0 = oi; }
       }
-      __syncthreads();
+      if (tid == 0) sh.tok = (int)i0;
     }
-    return (int)sh.ti[0];
+    __syncthreads();
+    return sh.tok;
   }
   if (active) {
     Cand cd;
