@@ -102,6 +102,23 @@ __device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag
   }
 }
 
+// v + v of lane ^ 8 / ^ 16 / ^ 32 in every lane, on DPP (row_ror:8) and the
+// gfx950 half-row / half-wave swaps (v_permlane16/32_swap) rather than
+// ds_bpermute: the same IEEE sums as a shuffle, at VALU latency.
+__device__ __forceinline__ float xor8_add(float v) { return v + dpp_mov<0x128>(v); }
+__device__ __forceinline__ float xor16_add(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Sum over the block (NW waves, fixed order); `sh` holds NW floats and must
 // not be reused before the next barrier.
 __device__ __forceinline__ float block_sum(float v, float* sh) {
@@ -145,8 +162,10 @@ __device__ __forceinline__ void mg_dots(const Pair* w, const float* xs, int Kp, 
   int gcur = wi0 / KpS - g0;
   auto flush = [&](int gl) {
     float v = acc;
-#pragma unroll
-    for (int m = GR; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+    static_assert(GR >= 8, "flush folds lane bits 3 and up");
+    if (GR <= 8) v = xor8_add(v);
+    if (GR <= 16) v = xor16_add(v);
+    if (GR <= 32) v = xor32_add(v);
     if (lane < GR) red[wv][gl * GR + lane] = v;
   };
 #pragma unroll
@@ -285,7 +304,7 @@ __device__ __forceinline__ float half_wave_max(float m) {
   m = fmaxf(m, dpp_mov<0x4E>(m));
   m = fmaxf(m, dpp_mov<0x141>(m));
   m = fmaxf(m, dpp_mov<0x140>(m));
-  return fmaxf(m, __shfl_xor(m, 16, 64));
+  return xor16_max(m);
 }
 
 // The gate/up GEMV input x (f32 in xs) as int8 planes: four threads per
@@ -786,7 +805,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         __syncthreads();
         stamp(a, b, l, 9);
         float g = gate_up_mfma(S, wgb, wgs);
-        g += __shfl_xor(g, 16, 64);
+        g = xor16_add(g);
         if (lane < 16) S.red[0][16 * wv + lane] = g;
         __syncthreads();
         stamp(a, b, l, 10);
@@ -859,9 +878,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       }
       if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 7);
-      acc += __shfl_xor(acc, 8, 64);
-      acc += __shfl_xor(acc, 16, 64);
-      acc += __shfl_xor(acc, 32, 64);
+      acc = xor32_add(xor16_add(xor8_add(acc)));
       if ((tid & 63) < 8) S.red[tid >> 6][j] = acc;
       __syncthreads();
       if (tid < 8) {
