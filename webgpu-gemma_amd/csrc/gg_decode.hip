@@ -976,11 +976,27 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       }
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const uint32_t oi = (uint32_t)__shfl_xor((int)bi, o, 64);
+  // wave max with the lowest index on ties: an associative, commutative
+  // choice (bv is never NaN), so any pairing order gives the same result;
+  // pairs over lane bits 0-5 on DPP and the half-row / half-wave swaps
+  auto take = [&](float ov, uint32_t oi) {
     if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  };
+  take(dpp_mov<0xB1>(bv), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)bi, 0xB1, 0xf, 0xf, false));
+  take(dpp_mov<0x4E>(bv), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)bi, 0x4E, 0xf, 0xf, false));
+  take(dpp_mov<0x141>(bv), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)bi, 0x141, 0xf, 0xf, false));
+  take(dpp_mov<0x128>(bv), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)bi, 0x128, 0xf, 0xf, false));
+  {
+    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(bi, bi, false, false);
+    const bool lo = ((lane >> 4) & 1) == 0;   // this lane's own value is r[0] in even rows, r[1] in odd
+    take(__uint_as_float(lo ? rv[1] : rv[0]), lo ? ri[1] : ri[0]);
+  }
+  {
+    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(bi, bi, false, false);
+    const bool lo = lane < 32;
+    take(__uint_as_float(lo ? rv[1] : rv[0]), lo ? ri[1] : ri[0]);
   }
   if (lane == 0) {
     S.cand_v[wv] = bv;
