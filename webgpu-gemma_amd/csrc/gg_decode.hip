@@ -3,16 +3,16 @@
 // The per-kernel token loop (gg_kernels.hip) pays a dependent kernel launch
 // for each of its 133 phases per token (2.4-3.7 us each on MI355X, measured
 // in a graph-replay chain), and each kernel starts its weight stream only
-// after its launch. Here 256 co-resident blocks (one per CU, 8 waves each)
+// after its launch. Here 256 co-resident blocks (one per CU, four waves each)
 // run every phase of every layer in one launch and hand outputs over through
 // LL words: a 64-bit {f32 value, 32-bit tag} pair written and polled with
 // device-scope relaxed atomics (global_store/load ... sc1). A word is valid
 // when its tag equals the (launch, layer) tag, so a consumer needs no flag,
 // no counter and no fence; an agent-scope release/acquire fence (a whole-L2
 // write-back or invalidate on this multi-XCD part) cost 32 us per phase in a
-// 256-block exchange, the LL exchange 2.2-2.5 us (1152 words) and 3.3 us
-// (6912 words). A block issues the weight loads of its next phase before it
-// polls that phase's input, so the weight stream overlaps the hand-off.
+// 256-block exchange. A block issues the weight loads of its next phase
+// before it polls that phase's input, so the weight stream overlaps the
+// hand-off.
 //
 // Phases per layer (engine.ts:766-795 order):
 //   Q   blocks [0, 192): 8-row groups of the fused QKV GEMV. Every block
@@ -20,13 +20,17 @@
 //       output (post-FFN norm + residual, engine.ts:794) into its own LDS:
 //       the residual is never exchanged, each block keeps an identical copy.
 //   A   blocks [192, 256): decode attention, block = (chunk of the span,
-//       query head), 16 chunks per head (fusedPerHeadNormRope, kvCacheStore,
+//       query head), 16 chunks per head in sliding-window layers, 32 in
+//       full-attention layers with blocks [0, 64) taking chunks 16..31 after
+//       their QKV rows (fusedPerHeadNormRope, kvCacheStore,
 //       attnScore/softmax/attnOutput, shaders.ts:209-325); chunk 0's block
-//       of each head merges the head's 16 chunk partials.
+//       of each head merges the head's chunk partials.
 //   O   blocks [0, H / 8): attention output projection.
-//   F1  all blocks: post-attention norm + residual + ffn_norm, gate/up GEMV,
-//       GeGLU (engine.ts:785-792).
-//   F2  blocks [0, H / 8): down projection (engine.ts:793).
+//   F   all blocks: post-attention norm + residual; blocks [0, I / 32):
+//       ffn_norm, the gate/up rows of 32 GeGLU outputs and their product
+//       with W_down's matching 32-wide input block, a split-K partial of the
+//       down output (engine.ts:785-793), both on int8 MFMA.
+//   R   blocks [0, H / 8): sums of the I / 32 down partials, fixed order.
 // Then DEC_FWD: block 0 finishes the pass (output norm, engine.ts:794-801);
 // DEC_STEP: every block takes one vocabulary class c (rows c + 256 k, the
 // stride classes of argmax / topk256, shaders.ts:327-384) of the tied LM
