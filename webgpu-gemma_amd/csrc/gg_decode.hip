@@ -37,7 +37,7 @@
 // head, from a class-major copy of the embedding, and hands over its
 // class candidate; block 0 selects the token (engine.ts:805-902).
 //
-// Every wait is bounded (a_spin_limit of s_memrealtime ticks): a block that
+// Every wait is bounded (a.spin_limit ticks of s_memrealtime): a block that
 // times out raises the host-visible flag and leaves, so the launch always
 // ends (the hand-off needs all 256 blocks resident: one per CU).
 #include <hip/hip_runtime.h>
