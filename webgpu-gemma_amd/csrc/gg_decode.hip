@@ -207,9 +207,9 @@ struct Smem {
   i32x4 xa4[6];                         // GeGLU output as int8 planes: [plane][32]
   i32x4 zq;                             // zero A operand of the lanes outside the planes
   float sact;                           // ... the GeGLU planes' scale
-  float res[kEPT * NT];                 // residual stream (H <= kDecMaxH), identical in every block
   float red[NW][kDecMaxRows];
   float shw[2][NW];
+  float sh4[4][NW];                     // resid_norm's four block sums
   int fail;
   float4 qs4[64], ks4[64], vs4[64];     // attention: normed + roped q, k; v
   float4 wo[NW][64];
@@ -239,22 +239,59 @@ __device__ __forceinline__ bool failed(Smem& S, bool ok) {
   return S.fail != 0;
 }
 
-// residual = pre_res + rmsNorm(v) * w (fusedNormAdd, shaders.ts:386-418) for
-// this thread's elements e = tid + NT i < H; returns sum of r^2 over the block.
-__device__ __forceinline__ void resid_update(Smem& S, const float* v, const float* w, int H, float eps, float* r,
-                                             int shi) {
-  const int tid = tidx();
-  float s1 = 0.f;
+// Four block sums at once (fixed order over the waves; one barrier).
+__device__ __forceinline__ void block_sum4(float (&v)[4], float (*sh)[NW]) {
+  const int id = tidx();
 #pragma unroll
-  for (int i = 0; i < kEPT; ++i)
-    if (tid + NT * i < H) s1 = fmaf(v[i], v[i], s1);
-  const float ri1 = rsq(block_sum(s1, S.shw[shi]) / (float)H + eps);
+  for (int k = 0; k < 4; ++k) v[k] = wave_sum_dpp(v[k]);
+  if ((id & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sh[k][id >> 6] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += sh[k][w];
+    v[k] = t;
+  }
+}
+
+// The residual stream r (this thread's elements e = tid + NT i < H, kept in
+// registers) += rmsNorm(v) * wpost (fusedNormAdd, shaders.ts:386-418) and,
+// with NORM, x = rmsNorm(r) * wpre into the GEMV input (rmsNorm,
+// shaders.ts:25-56), from one block reduction: with u = v * wpost and
+// a = 1 / rms(v), the new residual's sum of squares is
+// sum r^2 + 2 a sum r u + a^2 sum u^2, reduced together with sum v^2.
+template <bool NORM>
+__device__ __forceinline__ void resid_norm(Smem& S, const float* v, const float* wpost, const float* wpre, int H,
+                                           float eps, float* r) {
+  const int tid = tidx();
+  float sm[4] = {0.f, 0.f, 0.f, 0.f};
+  float u[kEPT];
 #pragma unroll
   for (int i = 0; i < kEPT; ++i) {
-    const int e = tid + NT * i;
-    if (e < H) {
-      r[i] = S.res[e] + (v[i] * w[i]) * ri1;
-      S.res[e] = r[i];
+    u[i] = v[i] * wpost[i];
+    if (tid + NT * i < H) {
+      sm[0] = fmaf(v[i], v[i], sm[0]);
+      sm[1] = fmaf(r[i], r[i], sm[1]);
+      sm[2] = fmaf(r[i], u[i], sm[2]);
+      sm[3] = fmaf(u[i], u[i], sm[3]);
+    }
+  }
+  block_sum4(sm, S.sh4);
+  const float ra = rsq(sm[0] / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i)
+    if (tid + NT * i < H) r[i] = r[i] + u[i] * ra;
+  if (NORM) {
+    const float ri = rsq((sm[1] + ra * (2.f * sm[2] + ra * sm[3])) / (float)H + eps);
+    float* xs = (float*)S.xs4;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      const int e = tid + NT * i;
+      if (e < H) xs[xs_index(e)] = (r[i] * wpre[i]) * ri;
     }
   }
 }
@@ -679,7 +716,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     const int e = tid + NT * i;
     if (e < H) {
       r[i] = embed_value(a.embd, a.kps_embd, a.embed_scale, token, e);
-      S.res[e] = r[i];
+    } else {
+      r[i] = 0.f;
     }
   }
 
@@ -733,16 +771,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       const bool ok = ll_wait<kEPT>(a.x_down, H, tag - 1, dv, lim);
       if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 1);
-      resid_update(S, dv, wpost, H, a.eps, r, 0);
+      if (qb) {
+        zero_red(S.red);
+        resid_norm<true>(S, dv, wpost, wn, H, a.eps, r);
+      } else {
+        resid_norm<false>(S, dv, wpost, wn, H, a.eps, r);
+      }
       if (b == 0) {
 #pragma unroll
         for (int i = 0; i < kEPT; ++i)
           if (tid + NT * i < H) a.hist[(size_t)(l - 1) * H + tid + NT * i] = r[i];
       }
-    }
-    if (qb) {
+    } else if (qb) {
       zero_red(S.red);
       norm_to_xs(S, r, wn, H, a.eps, 1);
+    }
+    if (qb) {
       __syncthreads();
       stamp(a, b, l, 8);
       mg_dots<8, 1>(wq, (const float*)S.xs4, Kq, a.kps_qkv, b, b * a.kps_qkv, a.kps_qkv, S.red);
@@ -800,10 +844,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       const bool ok = ll_wait<kEPT>(a.x_o, H, tag, ov, lim);
       if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 5);
-      resid_update(S, ov, wpa, H, a.eps, r, 0);
+      if (ffb) resid_norm<true>(S, ov, wpa, wffn, H, a.eps, r);
+      else resid_norm<false>(S, ov, wpa, wffn, H, a.eps, r);
       if (ffb) {
         const int lane = tid & 63, wv = tid >> 6;
-        norm_to_xs(S, r, wffn, H, a.eps, 1);
         __syncthreads();
         planes_from_xs(S, H);
         __syncthreads();
@@ -926,8 +970,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     load_norm(a.out_norm, H, wout);
     const bool ok = ll_wait<kEPT>(a.x_down, H, tagL, dv, lim);
     if (failed(S, ok)) { report_timeout(a); return; }
-    resid_update(S, dv, wpost, H, a.eps, r, 0);
-    norm_to_xs(S, r, wout, H, a.eps, 1);
+    resid_norm<true>(S, dv, wpost, wout, H, a.eps, r);
     __syncthreads();
     if (b == 0) {
       const float* xs = (const float*)S.xs4;
