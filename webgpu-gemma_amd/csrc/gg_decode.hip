@@ -239,6 +239,15 @@ __device__ __forceinline__ bool failed(Smem& S, bool ok) {
   return S.fail != 0;
 }
 
+// Failure check without a barrier, for polls whose consumer reaches a
+// barrier anyway: a block whose poll timed out carries on with whatever it
+// read (no index or branch depends on polled values; later polls of the
+// layer time out in turn, each bounded by the spin limit) and leaves,
+// reporting, at the end-of-layer check.
+__device__ __forceinline__ void soft_fail(Smem& S, bool ok) {
+  if (!ok) S.fail = 1;
+}
+
 // Four block sums at once (fixed order over the waves; one barrier).
 __device__ __forceinline__ void block_sum4(float (&v)[4], float (*sh)[NW]) {
   const int id = tidx();
@@ -769,7 +778,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       float dv[kEPT], wpost[kEPT];
       load_norm(norm_of(a, layer_view(a, l - 1), 5), H, wpost);
       const bool ok = ll_wait<kEPT>(a.x_down, H, tag - 1, dv, lim);
-      if (failed(S, ok)) { report_timeout(a); return; }
+      soft_fail(S, ok);
       stamp(a, b, l, 1);
       if (qb) {
         zero_red(S.red);
@@ -842,7 +851,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       load_norm(norm_of(a, Ly, 4), H, wpa);
       load_norm(norm_of(a, Ly, 1), H, wffn);
       const bool ok = ll_wait<kEPT>(a.x_o, H, tag, ov, lim);
-      if (failed(S, ok)) { report_timeout(a); return; }
+      soft_fail(S, ok);
       stamp(a, b, l, 5);
       if (ffb) resid_norm<true>(S, ov, wpa, wffn, H, a.eps, r);
       else resid_norm<false>(S, ov, wpa, wffn, H, a.eps, r);
@@ -924,7 +933,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         }
         if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
       }
-      if (failed(S, ok)) { report_timeout(a); return; }
+      soft_fail(S, ok);
       stamp(a, b, l, 7);
       acc = xor32_add(xor16_add(xor8_add(acc)));
       if ((tid & 63) < 8) S.red[tid >> 6][j] = acc;
@@ -938,6 +947,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       stamp(a, b, l, 11);
     }
     __syncthreads();
+    if (S.fail) { report_timeout(a); return; }
   }
 
   // ---- end of the pass: post-FFN norm + residual, output norm ----
@@ -969,9 +979,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     load_norm(norm_of(a, layer_view(a, a.L - 1), 5), H, wpost);
     load_norm(a.out_norm, H, wout);
     const bool ok = ll_wait<kEPT>(a.x_down, H, tagL, dv, lim);
-    if (failed(S, ok)) { report_timeout(a); return; }
+    soft_fail(S, ok);
     resid_norm<true>(S, dv, wpost, wout, H, a.eps, r);
     __syncthreads();
+    if (S.fail) { report_timeout(a); return; }
     if (b == 0) {
       const float* xs = (const float*)S.xs4;
 #pragma unroll
