@@ -44,6 +44,38 @@ def test_decode_path_selection(gpu, tiny_model):
     e.close()
 
 
+@pytest.mark.parametrize("path", ["fused", "graph"])
+def test_sampled_steps_select_exactly_from_their_logits(gpu, path):
+    """Sampling steps at the 270M shape (temperature 0.8, top-p 0.9,
+    repetition penalty 1.3, a seeded draw u per step): each step's token is
+    the oracle sampler's choice (engine.ts:862-901) over that step's own
+    logits, read back after the step, with the turn's penalty set (prompt and
+    every token chosen so far). On the persistent path the selection runs
+    inside the step's launch."""
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    e = engine(shape, synth.make_model(shape, seed=5), path)
+    assert e.decode_path() == path
+    prompt = synth.prompt_ids(48, seed=7, vocab=shape.vocab)
+    T, top_p, rep = 0.8, 0.9, 1.3
+    rng = np.random.default_rng(11)
+    e.penalty_reset()
+    e.penalty_add(prompt)
+    e.prefill(prompt, 0)
+    seen = set(int(t) for t in prompt)
+    tok = e.select(T, top_p, rep, float(rng.random()))
+    seen.add(tok)
+    pos = len(prompt)
+    for step in range(24):
+        u = float(rng.random())
+        nxt = e.step(tok, pos, T, top_p, rep, u)
+        vals, ids = orc.topk256(e.read(capi.READ_LOGITS))
+        want = orc.sample_candidates(vals, ids, sorted(seen), T, top_p, rep, u)
+        assert nxt == want, (path, step, nxt, want)
+        seen.add(nxt)
+        tok, pos = nxt, pos + 1
+    e.close()
+
+
 @pytest.mark.parametrize("shape_name", ["tiny", "270m"])
 def test_embedding_row_bit_exact(gpu, tiny_model, shape_name):
     """embeddingLookup (shaders.ts:2-23): (f32(q) * scale) * sqrt(f32(H)) of the
