@@ -32,12 +32,13 @@ def tiny_model():
 
 def test_decode_path_selection(gpu, tiny_model):
     """The persistent kernel is the default where its limits hold (4 query
-    heads, context <= 4096); longer contexts keep the graph path."""
+    heads, hidden <= 1280, 256 CUs), at any context length: contexts above
+    4096 run its long-span variant."""
     e = engine(synth.TINY.gemma3_mode(window=7), tiny_model)
     assert e.decode_path() == "fused"
     e.close()
     e = engine(synth.TINY.with_ctx(8192).gemma3_mode(window=7), tiny_model)
-    assert e.decode_path() == "graph"
+    assert e.decode_path() == "fused"
     e.close()
     e = engine(synth.TINY.gemma3_mode(window=7), tiny_model, "graph")
     assert e.decode_path() == "graph"
@@ -124,6 +125,52 @@ def test_decode_paths_agree_1b(gpu, mode):
                e.read(capi.READ_V_CACHE, l).reshape(shape.ctx, 256)[:pos]) for l in (0, 5, 11, 25)]
         runs[path] = (toks, hid, logits, kv)
         say("1b path", path, "tokens", toks[:6])
+        e.close()
+    (ta, ha, la, ka), (tb, hb, lb, kb) = runs["fused"], runs["graph"]
+    assert ta == tb
+    for x, y in zip(ha, hb):
+        for l in range(shape.layers):
+            assert rel(x[l], y[l]) < 1e-4, f"layer {l}"
+    for x, y in zip(la, lb):
+        assert rel(x, y) < 1e-4
+    for (k1, v1), (k2, v2) in zip(ka, kb):
+        assert rel(k1, k2) < 1e-4 and rel(v1, v2) < 1e-4
+
+
+@pytest.mark.parametrize("mode", ["gemma3", "reference"])
+def test_decode_paths_agree_1b_long_span(gpu, mode):
+    """Full 1B shape at context 8192: a 4090-id prompt (batched prefill, the
+    same K/V in both engines), then 24 greedy steps through positions
+    4090..4113 on each path. The persistent kernel's full-attention layers
+    switch from the 32-chunk layout to the 256-chunk four-head layout and its
+    64-block merge at position 4096 (every layer in reference mode); the
+    graph path runs its own long-span attention (k_attn_dec over 256 chunks
+    + k_attn_merge). Same tokens, every layer's hidden state and the logits
+    within 1e-4, the same K/V rows."""
+    shape = synth.GEMMA3_1B.with_ctx(8192)
+    shape = shape.gemma3_mode() if mode == "gemma3" else shape.reference_mode()
+    say("1b long-span paths build", mode)
+    t = synth.make_model(shape, seed=4)
+    prompt = synth.prompt_ids(4090, seed=4090, vocab=shape.vocab)
+    runs = {}
+    for path in ("fused", "graph"):
+        e = engine(shape, t, path, prefill_batch=2048)
+        assert e.decode_path() == path
+        e.prefill(prompt, 0)
+        tok = e.select()
+        toks, hid, logits = [tok], [], []
+        pos = len(prompt)
+        for step in range(24):
+            tok = e.step(tok, pos)
+            toks.append(tok)
+            pos += 1
+            if step in (4, 5, 6, 23):
+                hid.append(np.stack([e.read(capi.READ_LAYER_HIDDEN, l) for l in range(shape.layers)]))
+                logits.append(e.read(capi.READ_LOGITS))
+        kv = [(e.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:pos],
+               e.read(capi.READ_V_CACHE, l).reshape(shape.ctx, 256)[:pos]) for l in (0, 5, 11, 25)]
+        runs[path] = (toks, hid, logits, kv)
+        say("1b long-span path", path, "tokens", toks[:6])
         e.close()
     (ta, ha, la, ka), (tb, hb, lb, kb) = runs["fused"], runs["graph"]
     assert ta == tb

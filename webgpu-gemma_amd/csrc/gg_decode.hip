@@ -24,7 +24,10 @@
 //       full-attention layers with blocks [0, 64) taking chunks 16..31 after
 //       their QKV rows (fusedPerHeadNormRope, kvCacheStore,
 //       attnScore/softmax/attnOutput, shaders.ts:209-325); chunk 0's block
-//       of each head merges the head's chunk partials.
+//       of each head merges the head's chunk partials. Full-attention
+//       layers at spans above 4096 positions (k_decode<MODE, true>, for
+//       contexts above 4096): every block takes one of 256 chunks for all
+//       four heads (each K/V row read once), blocks [192, 256) merge.
 //   O   blocks [0, H / 8): attention output projection.
 //   F   all blocks: post-attention norm + residual; blocks [0, I / 32):
 //       ffn_norm, the gate/up rows of 32 GeGLU outputs and their product
@@ -695,9 +698,324 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
   return true;
 }
 
+// ---- long spans: full-attention layers past kDecMaxCtx positions ----------
+// Block b takes chunk b of kDecChunksL for all four query heads, so each K/V
+// row is read once per launch (one head per block would stream it four
+// times); blocks [192, 256) then merge the partials, block 192 + 16 h + s
+// dims 16 s .. 16 s + 15 of head h. Its LDS overlays the GEMV input x, which
+// is free between the QKV dots and the O poll (barriers on both sides).
+struct LongAttn {
+  float4 qs[kAttnMaxQ][64];       // normed + roped q of the four heads
+  float4 wo[NW][kAttnMaxQ][64];   // per-wave (o, max, sum) of each head
+  float wm[NW][kAttnMaxQ], wl[NW][kAttnMaxQ];
+  float mx[NW], ls[NW];           // merge: per-wave max of the chunk maxima, sum of f_c l_c
+  float f[kDecChunksL];           // merge: chunk weights f_c
+  float pm[NW][16];               // merge: per-wave sums of the 16-dim slice
+};
+static_assert(sizeof(LongAttn) <= sizeof(Smem::xs4), "long-span attention LDS exceeds the x buffer it overlays");
+
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = fmaxf(x, dpp_mov<0xB1>(x));
+  x = fmaxf(x, dpp_mov<0x4E>(x));
+  x = fmaxf(x, dpp_mov<0x141>(x));
+  return across8_max(x);
+}
+
+// RMSNorm (weights w) + NEOX RoPE of one head held as dims lane + 64 i
+// (fusedPerHeadNormRope, shaders.ts:209-227) into dst[256].
+__device__ __forceinline__ void head_norm_rope(float* x, const float* w, const float* cs, const float* sn,
+                                               float eps, int lane, float* dst) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
+  ss = wave_sum_dpp(ss);
+  const float ri = rsq(ss / (float)kHeadDim + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = (x[i] * w[i]) * ri;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float x0 = x[j], x1 = x[j + 2];
+    dst[lane + 64 * j] = x0 * cs[j] - x1 * sn[j];
+    dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
+  }
+}
+
+// Chunk c of a long span for the four query heads (the passes of
+// attention_block with every K/V row scored against all four heads):
+// wave w polls and normalises q of head w; in the block whose chunk holds
+// pos, wave 1 also takes this token's k and wave 2 its v, and the block
+// stores both into the cache. Partial of head h at (h * kDecChunksL + c).
+__device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, const LayerView& Ly, int l, int c,
+                                               int pos, uint32_t tag) {
+  LongAttn& LA = *reinterpret_cast<LongAttn*>(S.xs4);
+  const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
+  const long long lim = a.spin_limit;
+  int t_lo, ch, nch;
+  dec_span(pos, 0, kDecChunksL, &t_lo, &ch, &nch);
+  if (c >= nch) {   // past the span: empty partials (m = -inf)
+    for (int i = tid; i < kAttnMaxQ * kDecPart; i += NT) {
+      const int hh = i / kDecPart, d = i - hh * kDecPart;
+      ll_st(a.x_part + ((size_t)hh * kDecChunksL + c) * kDecPart + d, d == kHeadDim ? -INFINITY : 0.f, tag);
+    }
+    return true;
+  }
+  const int t0 = t_lo + c * ch;
+  const int t1 = min(t0 + ch, pos + 1);
+  const int npass = (t1 - t0 + 8 * NW - 1) / (8 * NW);
+  const int kv_last = max(pos - 1, 0);   // cache rows [0, pos) hold earlier tokens
+  const int pl = lane >> 3, oc = lane & 7;
+  const bool holder = (c == nch - 1);
+  float4 kr[8], vr[8];
+  auto load_k = [&](int p) {
+    const int t = min(t0 + 8 * NW * p + 8 * wv + pl, kv_last);
+    const GG_GLOBAL f32x4* kp = (const GG_GLOBAL f32x4*)(gmem(Ly.kc) + (size_t)t * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 v = __builtin_nontemporal_load(kp + oc + 8 * j);
+      kr[j] = make_float4(v.x, v.y, v.z, v.w);
+    }
+  };
+  auto load_v = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = min(t0 + 8 * NW * p + 8 * wv + i, kv_last);
+      const f32x4 v = __builtin_nontemporal_load((const GG_GLOBAL f32x4*)(gmem(Ly.vc) + (size_t)t * kHeadDim) + lane);
+      vr[i] = make_float4(v.x, v.y, v.z, v.w);
+    }
+  };
+  load_k(0);
+  load_v(0);
+  const GG_GLOBAL float* rt = gmem(Ly.rope) + (size_t)pos * kHeadDim;
+  float cs[2], sn[2], nq[4], nk[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cs[j] = rt[lane + 64 * j];
+    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
+  }
+  const GG_GLOBAL float* wq = gmem(norm_of(a, Ly, 2));
+  const GG_GLOBAL float* wk = gmem(norm_of(a, Ly, 3));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    nq[i] = wq[lane + 64 * i];
+    nk[i] = wk[lane + 64 * i];
+  }
+  // q of head wv (dims lane + 64 i); holder: wave 1 this token's k (same
+  // layout), wave 2 its v (dims 4 lane .. 4 lane + 3)
+  const bool extra = holder && (wv == 1 || wv == 2);
+  const uint64_t* qsrc = a.x_qkv + wv * kHeadDim;
+  const uint64_t* esrc = a.x_qkv + a.QD + (wv == 2 ? kHeadDim : 0);
+  bool ok = true;
+  float hx[4], ex[4];
+  {
+    const long long st0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      uint64_t w[4], e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = ll_ld(qsrc + lane + 64 * i);
+      if (extra) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = ll_ld(esrc + (wv == 2 ? 4 * lane + i : lane + 64 * i));
+      }
+      bool good = true;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) good &= ll_ok(w[i], tag);
+      if (extra) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) good &= ll_ok(e[i], tag);
+      }
+      if (good) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hx[i] = ll_val(w[i]);
+          ex[i] = extra ? ll_val(e[i]) : 0.f;
+        }
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - st0 > lim) { ok = false; break; }
+    }
+  }
+  if (ok) {
+    head_norm_rope(hx, nq, cs, sn, a.eps, lane, (float*)LA.qs[wv]);
+    if (holder && wv == 1) head_norm_rope(ex, nk, cs, sn, a.eps, lane, (float*)S.ks4);
+    if (holder && wv == 2) S.vs4[lane] = make_float4(ex[0], ex[1], ex[2], ex[3]);
+  }
+  if (failed(S, ok)) return false;
+  stamp(a, blockIdx.x, l, 12);
+  if (holder) {
+    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
+    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
+  }
+  if (c == 0) *(float4*)(a.q_dbg + (size_t)l * a.QD + 4 * tid) = LA.qs[wv][lane];
+
+  float4 qr[kAttnMaxQ][8];
+#pragma unroll
+  for (int hh = 0; hh < kAttnMaxQ; ++hh)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[hh][j] = LA.qs[hh][oc + 8 * j];
+  const float sl2 = a.attn_scale * 1.4426950408889634f;
+  float m[kAttnMaxQ], ls[kAttnMaxQ];
+  float4 o4[kAttnMaxQ];
+#pragma unroll
+  for (int hh = 0; hh < kAttnMaxQ; ++hh) {
+    m[hh] = -INFINITY;
+    ls[hh] = 0.f;
+    o4[hh] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int p = 0; p < npass; ++p) {
+    const int tb = t0 + 8 * NW * p + 8 * wv;
+    const int t = tb + pl;
+    if (t == pos) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kr[j] = S.ks4[oc + 8 * j];
+    }
+    float sc[kAttnMaxQ];
+#pragma unroll
+    for (int hh = 0; hh < kAttnMaxQ; ++hh) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d = fmaf(qr[hh][j].x, kr[j].x, d);
+        d = fmaf(qr[hh][j].y, kr[j].y, d);
+        d = fmaf(qr[hh][j].z, kr[j].z, d);
+        d = fmaf(qr[hh][j].w, kr[j].w, d);
+      }
+      d = group8_sum(d);
+      sc[hh] = t < t1 ? d * sl2 : -INFINITY;
+    }
+    if (p + 1 < npass) load_k(p + 1);
+    float pr[kAttnMaxQ], alpha[kAttnMaxQ];
+#pragma unroll
+    for (int hh = 0; hh < kAttnMaxQ; ++hh) {
+      const float mx = across8_max(sc[hh]);
+      const float mn = fmaxf(m[hh], mx);
+      alpha[hh] = (m[hh] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[hh] - mn);
+      pr[hh] = (sc[hh] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[hh] - mn);
+      ls[hh] = fmaf(ls[hh], alpha[hh], across8_sum(pr[hh]));
+      m[hh] = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (tb + i == pos) vr[i] = S.vs4[lane];
+#pragma unroll
+    for (int hh = 0; hh < kAttnMaxQ; ++hh) {
+      o4[hh].x *= alpha[hh];
+      o4[hh].y *= alpha[hh];
+      o4[hh].z *= alpha[hh];
+      o4[hh].w *= alpha[hh];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[hh]), 8 * i));
+        o4[hh].x = fmaf(pv, vr[i].x, o4[hh].x);
+        o4[hh].y = fmaf(pv, vr[i].y, o4[hh].y);
+        o4[hh].z = fmaf(pv, vr[i].z, o4[hh].z);
+        o4[hh].w = fmaf(pv, vr[i].w, o4[hh].w);
+      }
+    }
+    if (p + 1 < npass) load_v(p + 1);
+  }
+  // the four waves' (max, sum, o) per head, merged in a fixed order; wave
+  // hh writes head hh's partial
+#pragma unroll
+  for (int hh = 0; hh < kAttnMaxQ; ++hh) {
+    LA.wo[wv][hh][lane] = o4[hh];
+    if (lane == 0) {
+      LA.wm[wv][hh] = m[hh];
+      LA.wl[wv][hh] = ls[hh];
+    }
+  }
+  __syncthreads();
+  {
+    const int hh = wv;
+    const float M = fmaxf(fmaxf(LA.wm[0][hh], LA.wm[1][hh]), fmaxf(LA.wm[2][hh], LA.wm[3][hh]));
+    float L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = LA.wm[w][hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(LA.wm[w][hh] - M);
+      L = fmaf(f, LA.wl[w][hh], L);
+      const float4 v = LA.wo[w][hh][lane];
+      O.x = fmaf(f, v.x, O.x);
+      O.y = fmaf(f, v.y, O.y);
+      O.z = fmaf(f, v.z, O.z);
+      O.w = fmaf(f, v.w, O.w);
+    }
+    uint64_t* part = a.x_part + ((size_t)hh * kDecChunksL + c) * kDecPart;
+    ll_st(part + 4 * lane, O.x, tag);
+    ll_st(part + 4 * lane + 1, O.y, tag);
+    ll_st(part + 4 * lane + 2, O.z, tag);
+    ll_st(part + 4 * lane + 3, O.w, tag);
+    if (lane == 0) {
+      ll_st(part + kHeadDim, M, tag);
+      ll_st(part + kHeadDim + 1, L, tag);
+    }
+  }
+  return true;
+}
+
+// Merge of a long span: block hs = 16 h + s forms dims 16 s .. 16 s + 15 of
+// head h, o = sum_c f_c o_c / sum_c f_c l_c over the kDecChunksL partials
+// (f_c = 2^(m_c - max m), maxima in log2 units, empty chunks f_c = 0).
+// Thread t polls chunk t's (m, l) and dim t % 16 of chunks t / 16 + 16 k;
+// sums run in a fixed order (per thread in k, then xor trees over the
+// wave's chunk groups and the four waves in order).
+__device__ __forceinline__ bool merge_long(const DecodeArgs& a, Smem& S, int l, int hs, uint32_t tag) {
+  LongAttn& LA = *reinterpret_cast<LongAttn*>(S.xs4);
+  const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
+  const int h = hs >> 4, s = hs & 15, g = tid >> 4, d = tid & 15;
+  const uint64_t* base = a.x_part + (size_t)h * kDecChunksL * kDecPart;
+  constexpr int KC = kDecChunksL / 16;
+  float ov[KC], mt = -INFINITY, lt = 0.f;
+  bool ok = true;
+  {
+    const long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+      uint64_t w[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) w[k] = ll_ld(base + (size_t)(g + 16 * k) * kDecPart + 16 * s + d);
+      const uint64_t wm = ll_ld(base + (size_t)tid * kDecPart + kHeadDim);
+      const uint64_t wl = ll_ld(base + (size_t)tid * kDecPart + kHeadDim + 1);
+      bool good = ll_ok(wm, tag) & ll_ok(wl, tag);
+#pragma unroll
+      for (int k = 0; k < KC; ++k) good &= ll_ok(w[k], tag);
+      if (good) {
+#pragma unroll
+        for (int k = 0; k < KC; ++k) ov[k] = ll_val(w[k]);
+        mt = ll_val(wm);
+        lt = ll_val(wl);
+        break;
+      }
+      if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_limit) { ok = false; break; }
+    }
+  }
+  if (failed(S, ok)) return false;
+  stamp(a, blockIdx.x, l, 13);
+  const float wmx = wave_max_dpp(mt);
+  if (lane == 0) LA.mx[wv] = wmx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(LA.mx[0], LA.mx[1]), fmaxf(LA.mx[2], LA.mx[3]));
+  const float f = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
+  LA.f[tid] = f;
+  const float wls = wave_sum_dpp(f * lt);
+  if (lane == 0) LA.ls[wv] = wls;
+  __syncthreads();
+  const float L = ((LA.ls[0] + LA.ls[1]) + LA.ls[2]) + LA.ls[3];
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < KC; ++k) acc = fmaf(LA.f[g + 16 * k], ov[k], acc);
+  acc = xor32_add(xor16_add(acc));
+  if (lane < 16) LA.pm[wv][lane] = acc;
+  __syncthreads();
+  if (tid < 16) {
+    const float x = (((LA.pm[0][tid] + LA.pm[1][tid]) + LA.pm[2][tid]) + LA.pm[3][tid]) * (1.f / L);
+    ll_st(a.x_attn + h * kHeadDim + 16 * s + tid, x, tag);
+    if (l == a.L - 1) a.attn_out[h * kHeadDim + 16 * s + tid] = x;
+  }
+  return true;
+}
+
 }  // namespace
 
-template <int MODE>
+template <int MODE, bool LONG>
 __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   __shared__ Smem S;
   const int tid = threadIdx.x, b = blockIdx.x;
@@ -802,11 +1120,21 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       __syncthreads();
       if (tid < 8) ll_st(a.x_qkv + 8 * b + tid, red_row(S.red, tid), tag);
       stamp(a, b, l, 2);
-      // full-attention layers: blocks [0, 64) also take chunks 16..31
-      if (Ly.window == 0 && b < 64) {
+      if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
+        // long span: every block takes a chunk of the four heads
+        if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
+      } else if (Ly.window == 0 && b < 64) {
+        // full-attention layers: blocks [0, 64) also take chunks 16..31
         const int c = 16 + (b & 7) + 8 * (b >> 5), h = (b >> 3) & 3;
         if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a); return; }
       }
+      issue_ffn();
+    } else if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
+      // ---- A, long span: chunk b of the four heads, then the merge ----
+      if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
+      stamp(a, b, l, 2);
+      if (!merge_long(a, S, l, b - kDecQBlocks, tag)) { report_timeout(a); return; }
+      stamp(a, b, l, 3);
       issue_ffn();
     } else {
       // ---- A: attention (blocks [192, 256): chunks 0..15 of each head) ----
@@ -1119,17 +1447,24 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
 }
 
 int decode_occupancy() {
-  int n = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<DEC_STEP>, kDecThreads, 0);
-  return e == hipSuccess ? n : 0;
+  int n = 0, nl = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<DEC_STEP, false>, kDecThreads, 0);
+  const hipError_t el = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nl, k_decode<DEC_STEP, true>, kDecThreads, 0);
+  return e == hipSuccess && el == hipSuccess ? min(n, nl) : 0;
 }
 
 int launch_decode(int mode, const DecodeArgs& a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (mode == DEC_STEP && !a.lm) return (int)hipErrorInvalidValue;
   if (a.H > kDecMaxH || a.g_f > kDecMaxFBlocks) return (int)hipErrorInvalidValue;
-  if (mode == DEC_FWD) hipLaunchKernelGGL(k_decode<DEC_FWD>, dim3(kDecBlocks), dim3(kDecThreads), 0, s, a);
-  else hipLaunchKernelGGL(k_decode<DEC_STEP>, dim3(kDecBlocks), dim3(kDecThreads), 0, s, a);
+  const dim3 grid(kDecBlocks), block(kDecThreads);
+  if (a.long_ctx) {
+    if (mode == DEC_FWD) hipLaunchKernelGGL((k_decode<DEC_FWD, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<DEC_STEP, true>), grid, block, 0, s, a);
+  } else {
+    if (mode == DEC_FWD) hipLaunchKernelGGL((k_decode<DEC_FWD, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<DEC_STEP, false>), grid, block, 0, s, a);
+  }
   return (int)hipGetLastError();
 }
 

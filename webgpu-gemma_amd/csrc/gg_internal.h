@@ -234,7 +234,8 @@ constexpr int kDecPart = kHeadDim + 2;   // LL words of one chunk partial: o[256
 constexpr int kDecMaxRows = 128;     // rows of one phase a block may own
 constexpr int kDecMaxH = 1280;       // hidden sizes of the persistent kernel (its W_down rows per thread)
 constexpr int kDecMaxFBlocks = 256;  // FFN blocks: intermediate / 32 <= 256
-constexpr int kDecMaxCtx = 4096;     // 16 chunks per head cover spans up to 4096 positions
+constexpr int kDecMaxCtx = 4096;     // spans up to 4096: 16 / 32 chunks per head, one head per block
+constexpr int kDecChunksL = 256;     // longer spans of full-attention layers: chunk b of all four heads in block b
 enum DecMode { DEC_FWD = 0, DEC_STEP = 1 };
 
 // Every per-layer tensor kind is one layer-strided slab: layer l's copy is
@@ -267,7 +268,8 @@ struct DecodeArgs {
   const int32_t* tokens;
   // hand-off buffers (LL words)
   uint64_t* x_qkv;         // [NQKV]
-  uint64_t* x_part;        // [4][kDecChunksG][kDecPart]
+  uint64_t* x_part;        // chunk partials: head h, chunk c at (h * kDecChunksG + c) * kDecPart
+                           // (spans <= kDecMaxCtx) or (h * kDecChunksL + c) * kDecPart (longer)
   uint64_t* x_attn;        // [QD]
   uint64_t* x_o;           // [H]
   uint64_t* x_dpart;       // [g_f][H] partial down outputs
@@ -290,6 +292,9 @@ struct DecodeArgs {
   // needs no state upload before its launch (DEC_STEP only)
   int32_t in_use, in_pos, in_token;
   double in_temperature, in_top_p, in_rep_penalty, in_u;
+  // context_length > kDecMaxCtx: launches run k_decode<MODE, true>, whose
+  // full-attention layers take the 256-chunk path at spans above kDecMaxCtx
+  int32_t long_ctx;
 };
 constexpr int kDecEvents = 16;  // timeline events per (block, layer)
 int launch_decode(int mode, const DecodeArgs& a, void* stream);

@@ -228,7 +228,6 @@ struct ProbeScope {
 // Why the persistent decode kernel cannot run this model here ("" = it can).
 std::string fused_unsupported(gg_ctx* c) {
   if (c->NQ != kAttnMaxQ) return "needs 4 query heads";
-  if (c->CTX > kDecMaxCtx) return "needs context_length <= 4096 (16 attention chunks per head)";
   hipDeviceProp_t p;
   if (hipGetDeviceProperties(&p, c->device) != hipSuccess || p.multiProcessorCount < kDecBlocks)
     return "needs 256 compute units";
@@ -715,7 +714,7 @@ gg_ctx* gg_create(const gg_config* cfg) {
       dalloc(c, &c->s_norm, (size_t)c->L * N_NNORM * c->norm_stride * 4))
     return fail(0);
   // FFN copies of the persistent decode kernel, where its limits allow it
-  if (c->NQ == kAttnMaxQ && c->CTX <= kDecMaxCtx && c->H <= kDecMaxH && c->I % 32 == 0 &&
+  if (c->NQ == kAttnMaxQ && c->H <= kDecMaxH && c->I % 32 == 0 &&
       c->I / 32 <= kDecMaxFBlocks) {
     c->st_guf = (size_t)(c->I / 32) * gum_group_bytes(c->H);
     c->st_dcb = (size_t)(c->I / 32) * 34 * c->H;
@@ -974,7 +973,7 @@ int gg_finalize(gg_ctx* c) {
   if (c->fused) {
     DecodeArgs& d = c->dargs;
     // hand-off words; polled buffers hold kDecThreads * (words per thread)
-    const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunksG * kDecPart;
+    const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunksL * kDecPart;
     const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = 2048, w_dpart = (size_t)(c->I / 32) * c->H;
     const size_t w_cand = 512;
     c->xll_words = w_qkv + w_part + w_attn + 2 * w_h + w_dpart + w_cand;
@@ -1004,6 +1003,7 @@ int gg_finalize(gg_ctx* c) {
     d.rope_global = c->rope_global;
     d.swa_period = c->c.swa_period;
     d.window = c->c.sliding_window;
+    d.long_ctx = c->CTX > kDecMaxCtx;
     c->fused_step = c->V % 16384 == 0 && c->V <= 262144;
     if (c->fused_step) {
       GG_TRY(dalloc(c, &c->lm_cm, c->lay_embd.bytes()));
