@@ -138,24 +138,44 @@ def measured_traffic(name: str):
     return None
 
 
-def cpu_baseline(shape, tensors, pos0: int, budget_s: float, threads: int):
-    from oracle import oracle as orc
-    orc.set_threads(threads)
-    o = orc.OracleModel(shape, tensors)
-    n, t0 = 0, time.perf_counter()
-    tok = 2
+def _oracle_rate(o, pos0: int, budget_s: float, select: bool):
+    """Steps per second of the oracle over at least two steps and budget_s."""
+    n, t0, tok = 0, time.perf_counter(), 2
     while True:
         o.forward(tok, pos0 + n)
-        tok = o.select(0.0, 0.9, 1.0, 0.0)
+        if select:
+            tok = o.select(0.0, 0.9, 1.0, 0.0)
         n += 1
         el = time.perf_counter() - t0
         if n >= 2 and el >= budget_s:
-            break
+            return n, el
+
+
+def cpu_baseline(shape, tensors, pos0: int, budget_s: float, threads: int):
+    """The C oracle (a restatement of the reference pipeline in fp32) on the
+    host: greedy decode on `threads` cores (the reported value), the same on
+    one core, and forward passes without the LM head (the reference's
+    token-by-token prefill) whose rate gives an extrapolated 2048-token TTFT."""
+    from oracle import oracle as orc
+    orc.set_threads(threads)
+    o = orc.OracleModel(shape, tensors)
+    n, el = _oracle_rate(o, pos0, budget_s, True)
+    cores = orc.get_threads()
+    nf, elf = _oracle_rate(o, pos0 + n, max(2.0, budget_s / 5), False)
+    orc.set_threads(1)
+    n1, el1 = _oracle_rate(o, pos0 + n + nf, max(2.0, budget_s / 5), True)
+    orc.set_threads(threads)
     o.close()
-    return {"value": n / el, "unit": "tok/s", "cores": orc.get_threads(), "kind": "port",
+    return {"value": n / el, "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"{n} greedy decode steps (forward + LM head + argmax) of the 1B shape at positions "
                       f"{pos0}..{pos0 + n - 1} over a zero-filled KV cache, C oracle with OpenMP over "
-                      f"output rows, {el:.1f} s"}
+                      f"output rows, {el:.1f} s",
+            "value_1core": round(n1 / el1, 3),
+            "sample_1core": f"{n1} greedy decode steps on one core, {el1:.1f} s",
+            "prefill_tok_s": round(nf / elf, 3),
+            "ttft_2048_extrapolated_s": round(2048 * elf / nf, 1),
+            "sample_prefill": f"{nf} forward passes without the LM head on {cores} cores, {elf:.1f} s; "
+                              f"TTFT of a 2048-token prompt extrapolated from their rate"}
 
 
 def prefill_rows(args) -> int:
