@@ -308,7 +308,9 @@ def main():
         # timed by the engine's step events (forward = the launch)
         k_ms = dev_ms
         k_bytes = int(avg_bytes)
-        roof = {"bound": "hbm", "kernel": "k_decode<DEC_STEP> (persistent: 26 layers + LM head + selection)",
+        variant = "true" if ctx_len > 4096 else "false"   # the long-span variant above 4096 positions
+        roof = {"bound": "hbm",
+                "kernel": f"k_decode<DEC_STEP, {variant}> (persistent: 26 layers + LM head + selection)",
                 "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic("decode_step_traffic.txt") if default_workload else None,
