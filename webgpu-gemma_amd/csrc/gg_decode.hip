@@ -204,7 +204,10 @@ __device__ __forceinline__ float red_row(const float (*red)[kDecMaxRows], int t)
 }
 
 struct Smem {
-  float4 xs4[kMaxK / 64 * kXPad / 4];   // GEMV input x (K <= 8192)
+  union {
+    float4 xs4[kMaxK / 64 * kXPad / 4]; // GEMV input x (K <= 8192)
+    SelShared sel;                      // block 0's token selection, after its LM head has read x
+  };
   i32x4 xq4[kMaxKq * 12];               // FFN input as int8 planes: [pair column][plane][64]
   float4 xsc4[2][kMaxKq / 4];           // ... block scales: [block parity][pair column]
   i32x4 xa4[6];                         // GeGLU output as int8 planes: [plane][32]
@@ -220,7 +223,6 @@ struct Smem {
   float act[32];                        // the FFN block's GeGLU outputs
   float cand_v[NW];
   uint32_t cand_i[NW];
-  SelShared sel;
 };
 
 // Timeline stamp (profiling builds of a step only): thread 0 of each block
@@ -1015,7 +1017,7 @@ __device__ __forceinline__ bool merge_long(const DecodeArgs& a, Smem& S, int l, 
 
 }  // namespace
 
-template <int MODE, bool LONG>
+template <int MODE, bool LONG, bool SAMPLE>
 __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   __shared__ Smem S;
   const int tid = threadIdx.x, b = blockIdx.x;
@@ -1431,7 +1433,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     a.top[2 * tid] = __float_as_uint(m);
     a.top[2 * tid + 1] = id;
   }
-  const int tok = select_token(S.sel, m, id, tid < 256, sp, a.seen, a.V);
+  // greedy steps run the SAMPLE = false copy, which holds no sampler code
+  const int tok = SAMPLE ? select_token(S.sel, m, id, tid < 256, sp, a.seen, a.V)
+                         : select_greedy(S.sel, m, id, tid < 256);
   if (tid == 0) {
     a.st->out_token = tok;
     a.host_out[0] = tok;
@@ -1447,10 +1451,15 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
 }
 
 int decode_occupancy() {
-  int n = 0, nl = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<DEC_STEP, false>, kDecThreads, 0);
-  const hipError_t el = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nl, k_decode<DEC_STEP, true>, kDecThreads, 0);
-  return e == hipSuccess && el == hipSuccess ? min(n, nl) : 0;
+  int occ = 1 << 30;
+  const void* ks[] = {(const void*)k_decode<DEC_STEP, false, false>, (const void*)k_decode<DEC_STEP, false, true>,
+                      (const void*)k_decode<DEC_STEP, true, false>, (const void*)k_decode<DEC_STEP, true, true>};
+  for (const void* k : ks) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kDecThreads, 0) != hipSuccess) return 0;
+    occ = min(occ, n);
+  }
+  return occ;
 }
 
 int launch_decode(int mode, const DecodeArgs& a, void* stream) {
@@ -1458,12 +1467,18 @@ int launch_decode(int mode, const DecodeArgs& a, void* stream) {
   if (mode == DEC_STEP && !a.lm) return (int)hipErrorInvalidValue;
   if (a.H > kDecMaxH || a.g_f > kDecMaxFBlocks) return (int)hipErrorInvalidValue;
   const dim3 grid(kDecBlocks), block(kDecThreads);
-  if (a.long_ctx) {
-    if (mode == DEC_FWD) hipLaunchKernelGGL((k_decode<DEC_FWD, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_decode<DEC_STEP, true>), grid, block, 0, s, a);
+  // a step whose sampling options are arguments and greedy takes the copy
+  // without the sampler
+  const bool sample = !(a.in_use && a.in_temperature == 0.0 && a.in_rep_penalty <= 1.0);
+  if (mode == DEC_FWD) {
+    if (a.long_ctx) hipLaunchKernelGGL((k_decode<DEC_FWD, true, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<DEC_FWD, false, false>), grid, block, 0, s, a);
+  } else if (a.long_ctx) {
+    if (sample) hipLaunchKernelGGL((k_decode<DEC_STEP, true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<DEC_STEP, true, false>), grid, block, 0, s, a);
   } else {
-    if (mode == DEC_FWD) hipLaunchKernelGGL((k_decode<DEC_FWD, false>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_decode<DEC_STEP, false>), grid, block, 0, s, a);
+    if (sample) hipLaunchKernelGGL((k_decode<DEC_STEP, false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_decode<DEC_STEP, false, false>), grid, block, 0, s, a);
   }
   return (int)hipGetLastError();
 }

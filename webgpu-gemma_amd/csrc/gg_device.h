@@ -227,15 +227,29 @@ struct Cand {
   uint32_t id;
 };
 
+// Non-short-circuit (| and &): both fields are read before any test, so a
+// loop of comparisons against LDS entries has no branches and its loads
+// issue together.
 __device__ __forceinline__ bool cand_before(const Cand& x, const Cand& y) {
-  return x.val > y.val || (x.val == y.val && x.ord < y.ord);
+  return (x.val > y.val) | ((x.val == y.val) & (x.ord < y.ord));
 }
 
 struct SelShared {
-  float tv[256];
-  uint32_t ti[256];
+  union {
+    struct {
+      float tv[256];
+      uint32_t ti[256];
+    };
+    double q[256];      // sampling: probs[i] / sum, once the candidates are sorted
+  };
   Cand cs[256];
-  float probs[256];
+  union {
+    Cand ws[256];       // sampling: each wave's 64 candidates in sorted order
+    struct {
+      float probs[256];
+      double pre[257];  // sampling: pre[k] = probs[0] + ... + probs[k - 1], summed in order
+    };
+  };
   int tok;
 };
 
@@ -244,9 +258,14 @@ struct SelShared {
 // Greedy (temperature 0, rep_penalty <= 1): the argmax halving tree
 // (shaders.ts:351-357); otherwise the host sampler (engine.ts:862-901):
 // repetition penalty in f64 for ids in the bitmap, stable descending sort
-// (bitonic, ordered by value then slot), f32-stored exp of the scaled
-// differences, f64 sums, top-p cutoff and the walk with the draw u. Every
-// thread of the block calls it (it holds block barriers); the token is
+// (by value then slot: each candidate's rank within its wave's 64 by
+// comparison, plus a binary search of each other wave's sorted 64),
+// f32-stored exp of the scaled differences, f64 sums, top-p cutoff and the
+// walk with the draw u. The sums keep the host's sequential order: one pass
+// of running sums gives the total and every prefix (the top-p subset is the
+// prefix up to the cutoff), the quotients probs[i] / sum are formed in
+// parallel and only their cumulative sum and the walk run on one thread.
+// Every thread of the block calls it (it holds block barriers); the token is
 // returned to all threads.
 static __device__ SampleIn sample_of(const DevState* st) {
   SampleIn p;
@@ -258,42 +277,55 @@ static __device__ SampleIn sample_of(const DevState* st) {
   return p;
 }
 
-static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool active, const SampleIn& p,
-                                   const uint32_t* seen, int V) {
+// The sampling branch of select_token, out of line (one copy per kernel).
+static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, float m, uint32_t id, bool active,
+                                                               const SampleIn& p, const uint32_t* seen, int V);
+
+// Greedy selection alone (temperature 0, rep_penalty <= 1).
+static __device__ int select_greedy(SelShared& sh, float m, uint32_t id, bool active) {
   const int tid = threadIdx.x;
   if (active) {
     sh.tv[tid] = m;
     sh.ti[tid] = id;
   }
   __syncthreads();
-  const double T = p.temperature, rep = p.rep_penalty;
-  if (T == 0.0 && rep <= 1.0) {
-    // the tree of strides 128, 64, ..., 1 where slot t takes slot t + s when
-    // that value is strictly greater: the two widest levels from LDS, the
-    // rest in wave 0 (one barrier instead of eight, same comparisons)
-    if (tid < 64) {
-      float v0 = sh.tv[tid], v1 = sh.tv[tid + 64];
-      uint32_t i0 = sh.ti[tid], i1 = sh.ti[tid + 64];
-      const float v2 = sh.tv[tid + 128], v3 = sh.tv[tid + 192];
-      if (v2 > v0) { v0 = v2; i0 = sh.ti[tid + 128]; }
-      if (v3 > v1) { v1 = v3; i1 = sh.ti[tid + 192]; }
-      if (v1 > v0) { v0 = v1; i0 = i1; }
+  // the tree of strides 128, 64, ..., 1 where slot t takes slot t + s when
+  // that value is strictly greater: the two widest levels from LDS, the
+  // rest in wave 0 (one barrier instead of eight, same comparisons)
+  if (tid < 64) {
+    float v0 = sh.tv[tid], v1 = sh.tv[tid + 64];
+    uint32_t i0 = sh.ti[tid], i1 = sh.ti[tid + 64];
+    const float v2 = sh.tv[tid + 128], v3 = sh.tv[tid + 192];
+    if (v2 > v0) { v0 = v2; i0 = sh.ti[tid + 128]; }
+    if (v3 > v1) { v1 = v3; i1 = sh.ti[tid + 192]; }
+    if (v1 > v0) { v0 = v1; i0 = i1; }
 #pragma unroll
-      for (int s = 32; s > 0; s >>= 1) {
-        const float o = __shfl_down(v0, s, 64);
-        const uint32_t oi = (uint32_t)__shfl_down((int)i0, s, 64);
-        if (tid < s && o > v0) { v0 = o; i0 = oi; }
-      }
-      if (tid == 0) sh.tok = (int)i0;
+    for (int s = 32; s > 0; s >>= 1) {
+      const float o = __shfl_down(v0, s, 64);
+      const uint32_t oi = (uint32_t)__shfl_down((int)i0, s, 64);
+      if (tid < s && o > v0) { v0 = o; i0 = oi; }
     }
-    __syncthreads();
-    return sh.tok;
+    if (tid == 0) sh.tok = (int)i0;
   }
+  __syncthreads();
+  return sh.tok;
+}
+
+static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool active, const SampleIn& p,
+                                   const uint32_t* seen, int V) {
+  if (p.temperature == 0.0 && p.rep_penalty <= 1.0) return select_greedy(sh, m, id, active);
+  return select_sampled(sh, m, id, active, p, seen, V);
+}
+
+static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, float m, uint32_t id, bool active,
+                                                               const SampleIn& p, const uint32_t* seen, int V) {
+  const int tid = threadIdx.x;
+  const double T = p.temperature, rep = p.rep_penalty;
+  Cand cd;
+  cd.val = (double)m;
+  cd.ord = tid;
+  cd.id = id;
   if (active) {
-    Cand cd;
-    cd.val = (double)m;
-    cd.ord = tid;
-    cd.id = id;
     if (rep > 1.0 && p.seen_count > 0 && id < (uint32_t)V && ((seen[id >> 5] >> (id & 31)) & 1u)) {
       if (cd.val > 0) cd.val /= rep;
       else cd.val *= rep;
@@ -301,37 +333,83 @@ static __device__ int select_token(SelShared& sh, float m, uint32_t id, bool act
     sh.cs[tid] = cd;
   }
   __syncthreads();
-  for (int k = 2; k <= 256; k <<= 1) {
-    for (int jj = k >> 1; jj > 0; jj >>= 1) {
-      const int ixj = tid ^ jj;
-      if (active && ixj > tid) {
-        const bool up = (tid & k) == 0;
-        const Cand x = sh.cs[tid], y = sh.cs[ixj];
-        const bool sw = up ? cand_before(y, x) : cand_before(x, y);
-        if (sw) { sh.cs[tid] = y; sh.cs[ixj] = x; }
-      }
-      __syncthreads();
-    }
+  // the order is total (slots are distinct), so the ranks are a permutation:
+  // the rank within the wave's 64 sorts each wave's list into ws, then each
+  // other list contributes the count of its entries ordered before cd, found
+  // by a branch-free binary search (monotone predicate over a sorted list)
+  const int w0 = tid & ~63;
+  int rank = 0;
+  if (active) {
+#pragma unroll 8
+    for (int j = 0; j < 64; ++j) rank += cand_before(sh.cs[w0 + j], cd) ? 1 : 0;
+    sh.ws[w0 + rank] = cd;
   }
+  __syncthreads();
+  if (active) {
+    int cnt[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const Cand* L = sh.ws + 64 * w;
+      int pos = 0;
+#pragma unroll
+      for (int step = 32; step >= 1; step >>= 1) pos += cand_before(L[pos + step - 1], cd) ? step : 0;
+      pos += (pos == 63 && cand_before(L[63], cd)) ? 1 : 0;
+      cnt[w] = 64 * w == w0 ? 0 : pos;
+    }
+    rank += (cnt[0] + cnt[1]) + (cnt[2] + cnt[3]);
+    sh.cs[rank] = cd;
+  }
+  __syncthreads();
   if (T == 0.0) return (int)sh.cs[0].id;
   if (active) sh.probs[tid] = (float)exp((sh.cs[tid].val - sh.cs[0].val) / T);
   __syncthreads();
+  // thread 0's sequential passes read 16 values per LDS round trip (a
+  // load per step would wait out the LDS latency 256 times); within a group
+  // the same operations run in the same order, the exits become flags
+  constexpr int G = 16;
   if (tid == 0) {
-    double sum = 0.0;
-    for (int i = 0; i < 256; ++i) sum += (double)sh.probs[i];
+    double s = 0.0;
+    for (int c = 0; c < 256; c += G) {
+      float pv[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) pv[k] = sh.probs[c + k];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        sh.pre[c + k] = s;
+        s += (double)pv[k];
+      }
+    }
+    sh.pre[256] = s;
+  }
+  __syncthreads();
+  if (active) sh.q[tid] = (double)sh.probs[tid] / sh.pre[256];
+  __syncthreads();
+  if (tid == 0) {
     double cum = 0.0;
     int cutoff = 256;
-    for (int i = 0; i < 256; ++i) {
-      cum += (double)sh.probs[i] / sum;
-      if (cum >= p.top_p) { cutoff = i + 1; break; }
+    for (int c = 0; c < 256 && cutoff == 256; c += G) {
+      double qv[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) qv[k] = sh.q[c + k];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        cum += qv[k];
+        cutoff = (cutoff == 256 && cum >= p.top_p) ? c + k + 1 : cutoff;
+      }
     }
-    double subset = 0.0;
-    for (int i = 0; i < cutoff; ++i) subset += (double)sh.probs[i];
-    double r = p.u * subset;
+    double r = p.u * sh.pre[cutoff];
     int pick = -1;
-    for (int i = 0; i < cutoff; ++i) {
-      r -= (double)sh.probs[i];
-      if (r <= 0) { pick = i; break; }
+    for (int c = 0; c < cutoff && pick < 0; c += G) {
+      float pv[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) pv[k] = sh.probs[c + k];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const bool on = (c + k < cutoff) & (pick < 0);
+        const double rn = r - (double)pv[k];
+        r = on ? rn : r;
+        pick = (on & (rn <= 0)) ? c + k : pick;
+      }
     }
     if (pick < 0) pick = cutoff - 1;
     sh.tok = (int)sh.cs[pick].id;
