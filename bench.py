@@ -310,7 +310,8 @@ def main():
         k_bytes = int(avg_bytes)
         variant = "true" if ctx_len > 4096 else "false"   # the long-span variant above 4096 positions
         roof = {"bound": "hbm",
-                "kernel": f"k_decode<DEC_STEP, {variant}> (persistent: 26 layers + LM head + selection)",
+                "kernel": f"k_decode<DEC_STEP, {variant}, false> (persistent, greedy copy: 26 layers + LM head + "
+                          "selection)",
                 "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic("decode_step_traffic.txt") if default_workload else None,
