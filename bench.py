@@ -237,6 +237,8 @@ def main():
                     help="fill the context token by token (the reference's prefillBatched) instead of batched")
     ap.add_argument("--decode", default="fused", choices=["fused", "graph"],
                     help="decode path: the persistent kernel (one launch per token) or one kernel per phase")
+    ap.add_argument("--sync-steps", action="store_true",
+                    help="time synchronous gg_step calls instead of the pipelined loop the JS host runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the batch-1 token loop runs on "
@@ -279,12 +281,33 @@ def main():
         tok = e.step(tok, pos)
         pos += 1
     pos_timed0 = pos
+    if args.sync_steps:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            tok = e.step(tok, pos)
+            pos += 1
+        elapsed = time.perf_counter() - t0
+    else:
+        # the JavaScript host's generate() loop: one step queued ahead, each
+        # step taking the previous step's id on the device (gg_step_submit
+        # with token -1); every timed step is collected by the host
+        e.step_submit(tok, pos)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            e.step_submit(-1, pos + 1)
+            tok = e.step_collect()
+            pos += 1
+        elapsed = time.perf_counter() - t0
+        e.step_collect()   # the step queued past the timed ones
+        pos += 1
+    pos_timed1 = pos_timed0 + args.steps
+    # synchronous gg_step calls (one host round trip per step), for reference
+    n_sync = min(args.steps, 128)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(n_sync):
         tok = e.step(tok, pos)
         pos += 1
-    elapsed = time.perf_counter() - t0
-    pos_timed1 = pos
+    sync_ms = (time.perf_counter() - t0) * 1e3 / n_sync
     # device time per step from the engine's step events, in a separate
     # untimed loop (the three event records cost ~9 us of device time a step)
     e.set_timing(True)
@@ -354,7 +377,11 @@ def main():
         "config": {"workload": f"gemma3-1b-q8_0-greedy-decode-after-{args.ctx}", "ctx_prefilled": args.ctx,
                    "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
                    "gemma3 (22 local layers window 512 theta 1e4, 4 global theta 1e6)",
-                   "positions": [pos_timed0, pos_timed1 - 1], "decode_path": decode_path},
+                   "positions": [pos_timed0, pos_timed1 - 1], "decode_path": decode_path,
+                   "step_loop": "gg_step per step" if args.sync_steps else
+                   "gg_step_submit one step ahead (input id taken on the device) + gg_step_collect, as the "
+                   "JavaScript host's generate() runs"},
+        "ms_per_step_sync": round(sync_ms, 4),
         "roofline": roof,
         "step_roofline": {"bytes_per_token": int(avg_bytes),
                           "achieved_GBs": round(avg_bytes / (ms_per_step * 1e-3) / 1e9, 1),

@@ -120,6 +120,26 @@ int gg_select(gg_ctx* ctx, const gg_sample* s, double u, int32_t* out_token);
 int gg_step(gg_ctx* ctx, int32_t token, int32_t pos, const gg_sample* s, double u,
             int32_t* out_token);
 
+/* Pipelined decode steps. No counterpart in the reference, whose generate()
+ * loop (engine.ts:1001-1030) awaits each step's id before encoding the
+ * next; the host uses these in that loop to keep one step queued ahead.
+ *
+ * gg_step_submit queues a step (forward + select, as gg_step) at `pos` and
+ * returns without waiting. Its input is `token`; with token < 0 it is the
+ * id that the previously submitted step (or the last gg_step / gg_select)
+ * selects, read on the device, so the step can be queued before that id
+ * reaches the host. gg_step_collect waits for the oldest submitted step and
+ * returns its id.
+ *
+ * At most two steps may be outstanding. Every other call except
+ * gg_destroy fails with GG_ERR_INVALID while any is. A step that is
+ * collected and not used leaves its K/V row at `pos` and its id in the
+ * penalty set; the next prefill at `pos` overwrites the row, and
+ * gg_penalty_reset clears the set. Without the persistent decode kernel's
+ * single-launch step, gg_step_submit runs the step before it returns. */
+int gg_step_submit(gg_ctx* ctx, int32_t token, int32_t pos, const gg_sample* s, double u);
+int gg_step_collect(gg_ctx* ctx, int32_t* out_token);
+
 /* Repetition-penalty set (the reference's Set(allTokens), engine.ts:868-876,
  * 989, 994, 1021): cleared per turn, filled with the turn's prompt ids. */
 int gg_penalty_reset(gg_ctx* ctx);
@@ -164,8 +184,8 @@ int gg_probe_elapsed(gg_ctx* ctx, float* ms);
 int gg_probe_overhead(gg_ctx* ctx, float* ms);
 
 /* Decode path of the per-token forward passes. GG_DECODE_FUSED (the default
- * where the model and device allow it: 4 query heads, context_length <=
- * 4096, 256 compute units) runs a whole forward pass -- and, for a
+ * where the model and device allow it: 4 query heads, hidden <= 1280, 256
+ * compute units) runs a whole forward pass -- and, for a
  * vocabulary that is a multiple of 16384, the LM head and the selection --
  * as one launch of a persistent kernel whose 256 blocks hand their outputs
  * to each other in device memory; GG_DECODE_GRAPH replays one kernel per

@@ -141,6 +141,36 @@ class FakeGG {
   async step(ctx, tok, pos, t, p, r, u) { this.rec('step', [tok, pos, t, p, r, u]); return this.script.shift(); }
 }
 
+// Fakes whose step results depend only on the position (a table), so a
+// sequential and a pipelined run of the same turn see the same ids.
+class TableGG extends FakeGG {
+  constructor(first, table) {
+    super([]);
+    this.first = first.slice();   // the id select() returns, per turn
+    this.table = table;           // pos -> id of the step at pos
+  }
+  async select(ctx, t, p, r, u) { this.rec('select', [t, p, r, u]); return this.first.shift(); }
+  async step(ctx, tok, pos, t, p, r, u) { this.rec('step', [tok, pos, t, p, r, u]); return this.table(pos); }
+}
+class PipeGG extends TableGG {
+  constructor(first, table) {
+    super(first, table);
+    this.queue = [];
+    this.last = -1;
+  }
+  select(ctx, t, p, r, u) {
+    return super.select(ctx, t, p, r, u).then((id) => { this.last = id; return id; });
+  }
+  stepSubmit(ctx, tok, pos, t, p, r, u) {
+    assert.ok(this.queue.length < 2, 'at most two steps outstanding');
+    const input = tok < 0 ? this.last : tok;   // -1: the previous step's id, "on the device"
+    this.rec('step', [input, pos, t, p, r, u]);
+    this.last = this.table(pos);
+    this.queue.push(this.last);
+  }
+  async stepCollect() { this.rec('collect', []); return this.queue.shift(); }
+}
+
 async function collect(gen) {
   const out = [];
   for await (const s of gen) out.push(s);
@@ -257,6 +287,57 @@ async function engineTests() {
     await collect(r.e.generate({}));
     const last = r.gg.calls.filter((c) => c[0] === 'step').pop();
     assert.strictEqual(last[2], 64 - 2);      // pos >= contextLength - 1 ends the turn
+  });
+  await test('engine: the pipelined loop (one step queued ahead) matches the sequential loop', async () => {
+    const endCall = W('<end_function_call>');
+    const scenarios = [
+      { name: 'stop id', opts: { temperature: 0 }, table: (p) => (p === 20 ? 106 : 210 + (p % 5)) },
+      { name: 'function call end', opts: { temperature: 0 }, table: (p) => (p === 18 ? endCall : 211) },
+      { name: 'maxTokens', opts: { temperature: 0.7, maxTokens: 4 }, table: () => 212 },
+      { name: 'end of context', opts: { temperature: 0 }, table: () => 213 },
+      { name: 'abort after two ids', opts: { temperature: 0 }, table: () => 214, abortAfter: 2 },
+    ];
+    let dropped = 0;
+    for (const sc of scenarios) {
+      const runs = [];
+      for (const Kind of [TableGG, PipeGG]) {
+        const gg = new Kind([215, 216], sc.table);
+        let draws = 0;
+        const e = await createGemmaEngine({ model: ggufPath, backend: gg, contextLength: 64,
+          random: () => { draws++; return 0.25; } });
+        const outs = [];
+        for (const text of ['Hello', 'the']) {
+          e.addUserMessage(text);
+          const signal = { aborted: false };
+          const got = [];
+          for await (const s of e.generate(Object.assign({ signal: signal }, sc.opts))) {
+            got.push(s);
+            if (sc.abortAfter && got.length === sc.abortAfter) signal.aborted = true;
+          }
+          outs.push({ got: got, kv: e.kvPosition });
+        }
+        const steps = gg.calls.filter((c) => c[0] === 'step').map((c) => [c[1], c[2]]);
+        const collects = gg.calls.filter((c) => c[0] === 'collect').length;
+        runs.push({ outs: outs, steps: steps, collects: collects, draws: draws, pipe: Kind === PipeGG });
+      }
+      const [seq, pipe] = runs;
+      assert.deepStrictEqual(pipe.outs, seq.outs, sc.name);
+      // every sequential step appears, in order, with its input id and position; the
+      // pipelined run adds at most one queued step per turn, collected and dropped
+      let i = 0;
+      const extra = [];
+      for (const st of pipe.steps) {
+        if (i < seq.steps.length && st[0] === seq.steps[i][0] && st[1] === seq.steps[i][1]) i++;
+        else extra.push(st);
+      }
+      assert.strictEqual(i, seq.steps.length, sc.name + ': sequential steps missing');
+      assert.ok(extra.length <= 2, sc.name + ': at most one dropped step per turn');
+      assert.strictEqual(pipe.collects, pipe.steps.length, sc.name + ': every queued step is collected');
+      if (sc.opts.temperature > 0) assert.strictEqual(pipe.draws, seq.draws + extra.length, sc.name);
+      assert.ok(pipe.steps.length > 0, sc.name);
+      dropped += extra.length;
+    }
+    assert.ok(dropped > 0);   // the queued-ahead path ran and dropped its extra steps
   });
   await test('engine: context overflow resets the KV cache and keeps only the last user message', async () => {
     const { e, gg } = await mk([210, 106, 210, 106]);

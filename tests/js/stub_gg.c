@@ -149,3 +149,20 @@ int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u,
   *out = token + 1;
   return GG_OK;
 }
+
+/* pipelined steps: submit records the id, collect sleeps like a step */
+static int32_t g_pending = -1;
+int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u) {
+  (void)pos, (void)s, (void)u;
+  enter(c, "step_submit");
+  leave(c, "step_submit", 0);
+  g_pending = token < 0 ? g_pending + 1 : token + 1;
+  return GG_OK;
+}
+
+int gg_step_collect(gg_ctx* c, int32_t* out) {
+  enter(c, "step_collect");
+  leave(c, "step_collect", 300);
+  *out = g_pending;
+  return GG_OK;
+}

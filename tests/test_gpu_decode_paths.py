@@ -183,6 +183,48 @@ def test_decode_paths_agree_1b_long_span(gpu, mode):
         assert rel(k1, k2) < 1e-4 and rel(v1, v2) < 1e-4
 
 
+@pytest.mark.parametrize("path", ["fused", "graph"])
+def test_pipelined_steps_match_sequential_steps(gpu, path):
+    """gg_step_submit / gg_step_collect with one step queued ahead, each next
+    step taking its input id on the device (token -1), give the ids of
+    sequential gg_step calls with the same draws: greedy, then sampled with a
+    repetition penalty, at the 270M shape. Other calls are refused while a
+    step is outstanding; a step queued past the last one is collected and
+    dropped."""
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    t = synth.make_model(shape, seed=5)
+    prompt = synth.prompt_ids(48, seed=48, vocab=shape.vocab)
+    a, b = engine(shape, t, path), engine(shape, t, path)
+    for opts in ((0.0, 0.9, 1.0), (0.8, 0.9, 1.3)):
+        us = [float(x) for x in np.random.default_rng(3).random(25)]
+        ids = {}
+        for name, e in (("seq", a), ("pipe", b)):
+            e.reset_kv()
+            e.penalty_reset()
+            e.penalty_add(prompt)
+            e.prefill(prompt, 0)
+            tok = e.select(*opts, us[0])
+            out = [tok]
+            if name == "seq":
+                for k in range(24):
+                    tok = e.step(tok, 48 + k, *opts, us[k + 1])
+                    out.append(tok)
+            else:
+                e.step_submit(tok, 48, *opts, us[1])
+                for k in range(24):
+                    e.step_submit(-1, 48 + k + 1, *opts, us[min(k + 2, 24)])
+                    out.append(e.step_collect())
+                    if k == 3:
+                        with pytest.raises(capi.GGError) as ex:
+                            e.read(capi.READ_HIDDEN)
+                        assert ex.value.code == capi.GG_ERR_INVALID
+                e.step_collect()   # the step queued past the last one
+            ids[name] = out
+        assert ids["pipe"] == ids["seq"], opts
+    a.close()
+    b.close()
+
+
 def test_persistent_kernel_timeout_is_reported(gpu, tiny_model, monkeypatch):
     """Every hand-off wait of the persistent kernel is bounded; a wait that
     runs out raises a host-visible flag and the block leaves, so the launch

@@ -1,8 +1,11 @@
 """The JavaScript host on the GPU through the Node-API binding: two generate()
 turns (greedy, then sampled with a seeded draw) on a tiny GGUF written by
-gemma_amd.gguf. The binding calls the host made are replayed through the
-Python C-ABI binding and must give the same ids; the greedy turn must also
-match the oracle."""
+gemma_amd.gguf. generate() keeps one step queued ahead (stepSubmit /
+stepCollect, each step taking the previous id on the device); every
+collected step is logged with its input id resolved. The binding calls the
+host made are replayed through the Python C-ABI binding as sequential steps
+and must give the same ids (a step queued past a turn's end included); the
+greedy turn must also match the oracle."""
 import json
 import os
 import shutil
@@ -69,6 +72,6 @@ def test_js_host_on_gpu(gpu, tmp_path, attention):
     o.close()
     # positions: the second turn's prefill starts where the first turn's KV ends
     pf = [c for c in log if c["op"] == "prefill"]
-    greedy_writes = sum(1 for c in sel if c["op"] == "step")
+    greedy_writes = sum(1 for c in sel if c["op"] == "step" and not c.get("dropped"))
     assert pf[1]["pos"] == len(pf[0]["ids"]) + greedy_writes
     assert pf[1]["ids"][0] != 2        # the turn suffix has no BOS

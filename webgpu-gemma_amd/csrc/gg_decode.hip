@@ -1033,7 +1033,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   const bool args_in = MODE == DEC_STEP && a.in_use != 0;
   const int pos = args_in ? a.in_pos : st->pos;
   const int cur = args_in ? -1 : st->cursor;
-  const int token = args_in ? a.in_token : cur < 0 ? st->token : a.tokens[cur];
+  const int token = args_in ? (a.in_token >= 0 ? a.in_token : st->out_token) : cur < 0 ? st->token : a.tokens[cur];
   const uint32_t base = epoch * (uint32_t)(a.L + 2);
   __syncthreads();
 
@@ -1438,7 +1438,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
                          : select_greedy(S.sel, m, id, tid < 256);
   if (tid == 0) {
     a.st->out_token = tok;
-    a.host_out[0] = tok;
+    a.host_out[a.out_slot] = tok;
     if (tok >= 0 && tok < a.V) {
       // no-return atomic OR: no load round trip at the end of the launch
       __hip_atomic_fetch_or(a.seen + (tok >> 5), 1u << (tok & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -284,13 +284,15 @@ struct DecodeArgs {
   float* logits;           // DEC_STEP: [V] class-major
   uint32_t* top;           // [256] x {f32 bits, id}
   uint32_t* seen;          // penalty bitmap
-  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag
+  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag, [4..5] pipelined tokens
   long long spin_limit;    // s_memrealtime ticks (100 MHz) one hand-off may wait
   long long* timeline;     // optional [256][L][kDecEvents] s_memrealtime stamps (null: off)
   // in_use != 0: this launch's position, token and sampling parameters are
   // these arguments rather than DevState's host-written head, so a decode step
-  // needs no state upload before its launch (DEC_STEP only)
-  int32_t in_use, in_pos, in_token;
+  // needs no state upload before its launch (DEC_STEP only); in_token < 0:
+  // the id the previous launch selected (DevState::out_token); the id is
+  // written to host_out[out_slot]
+  int32_t in_use, in_pos, in_token, out_slot;
   double in_temperature, in_top_p, in_rep_penalty, in_u;
   // context_length > kDecMaxCtx: launches run k_decode<MODE, true>, whose
   // full-attention layers take the 256-chunk path at spans above kDecMaxCtx

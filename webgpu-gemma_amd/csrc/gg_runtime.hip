@@ -139,6 +139,13 @@ struct gg_ctx {
   hipGraphExec_t g_ffwd = nullptr, g_fstep = nullptr;
   uint64_t dec_launches = 0;          // since the hand-off words were last cleared
   size_t xll_words = 0;
+  // pipelined steps (gg_step_submit / gg_step_collect): a FIFO of at most two
+  int pipe_n = 0, pipe_head = 0;      // outstanding steps, slot of the oldest
+  bool pipe_launched[2] = {false, false};   // slot's step is a launch in flight (else its id is known)
+  int32_t pipe_tok[2] = {0, 0};       // ids of steps that ran synchronously
+  hipEvent_t pipe_ev[2] = {nullptr, nullptr};
+  bool have_prev = false;             // a selection has run: a step may take its id on the device
+  int32_t last_tok = 0;               // ... that id, when the host knows it
   bool logits_cm = false;             // the last logits are in class-major order
   long long* timeline = nullptr;      // GG_DEC_TIMELINE=1: phase stamps of the last launch
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -206,6 +213,14 @@ int check_ready(gg_ctx* c) {
   if (!c) return GG_ERR_INVALID;
   if (c->lost) return set_err(c, GG_ERR_DEVICE_LOST, "device lost: recreate the context");
   if (!c->finalized) return set_err(c, GG_ERR_INVALID, "context not finalized");
+  return GG_OK;
+}
+
+// Ready, and no pipelined step outstanding (calls that use the device
+// state or buffers must not interleave with them).
+int check_idle(gg_ctx* c) {
+  GG_TRY(check_ready(c));
+  if (c->pipe_n > 0) return set_err(c, GG_ERR_INVALID, "pipelined steps outstanding: gg_step_collect them first");
   return GG_OK;
 }
 
@@ -957,6 +972,9 @@ int gg_finalize(gg_ctx* c) {
   memset(c->h_st, 0, sizeof(DevState));
   // timing events only: no system-scope fence (an L2 write-back) per record
   for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->ev[i], hipEventDisableSystemFence));
+  // completion of pipelined steps: the host reads each step's id from mapped
+  // memory after its event, so these keep the system-scope release
+  for (int i = 0; i < 2; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->pipe_ev[i], hipEventDisableTiming));
   if (c->probe_kind != GG_PROBE_NONE)
     // timing-only events: no system-scope fence (cache write-back/invalidate)
     // around the bracketed launch
@@ -1068,7 +1086,7 @@ int gg_finalize(gg_ctx* c) {
 }
 
 int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   if (n < 0 || (n > 0 && !tokens) || start_pos < 0 || (long long)start_pos + n > c->CTX)
     return set_err(c, GG_ERR_INVALID, "prefill range outside the context");
   if (n == 0) return GG_OK;
@@ -1156,31 +1174,98 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
 }
 
 int gg_select(gg_ctx* c, const gg_sample* s, double u, int32_t* out_token) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   if (!s || !out_token) return set_err(c, GG_ERR_INVALID, "null argument");
-  return select_impl(c, s, u, out_token, false);
+  GG_TRY(select_impl(c, s, u, out_token, false));
+  c->have_prev = true;
+  c->last_tok = *out_token;
+  return GG_OK;
 }
 
-int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u, int32_t* out_token) {
-  GG_TRY(check_ready(c));
+static int step_impl(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u, int32_t* out_token) {
   if (!s || !out_token) return set_err(c, GG_ERR_INVALID, "null argument");
   if (token < 0 || token >= c->V) return set_err(c, GG_ERR_INVALID, "token id out of range");
   if (pos < 0 || pos >= c->CTX) return set_err(c, GG_ERR_INVALID, "position outside the context");
   c->h_st->pos = pos;
   c->h_st->cursor = -1;   // embed DevState.token: one state upload per step
   c->h_st->token = token;
-  return select_impl(c, s, u, out_token, true);
+  GG_TRY(select_impl(c, s, u, out_token, true));
+  c->have_prev = true;
+  c->last_tok = *out_token;
+  return GG_OK;
+}
+
+int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u, int32_t* out_token) {
+  GG_TRY(check_idle(c));
+  return step_impl(c, token, pos, s, u, out_token);
+}
+
+int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u) {
+  GG_TRY(check_ready(c));
+  if (!s) return set_err(c, GG_ERR_INVALID, "null argument");
+  if (token >= c->V) return set_err(c, GG_ERR_INVALID, "token id out of range");
+  if (token < 0 && !c->have_prev) return set_err(c, GG_ERR_INVALID, "no selected id to take: select or step first");
+  if (pos < 0 || pos >= c->CTX) return set_err(c, GG_ERR_INVALID, "position outside the context");
+  if (c->pipe_n >= 2) return set_err(c, GG_ERR_INVALID, "two steps outstanding: gg_step_collect first");
+  const int slot = (c->pipe_head + c->pipe_n) & 1;
+  if (c->fused && c->fused_step) {
+    // one launch, queued behind the previous one; with token < 0 it embeds
+    // the id that launch selects (DevState::out_token, read on the device)
+    GG_TRY(fused_launch_begin(c));
+    DecodeArgs a = c->dargs;
+    a.in_use = 1;
+    a.in_pos = pos;
+    a.in_token = token;
+    a.in_temperature = s->temperature;
+    a.in_top_p = s->top_p;
+    a.in_rep_penalty = s->rep_penalty;
+    a.in_u = u;
+    a.out_slot = 4 + slot;
+    GG_TRY(launch_rc(c, launch_decode(DEC_STEP, a, c->stream), "persistent decode kernel"));
+    GG_HIP(c, hipEventRecord(c->pipe_ev[slot], c->stream));
+    c->pipe_launched[slot] = true;
+    c->logits_cm = true;
+    c->timed = false;
+    c->probed = true;
+  } else {
+    // no single-launch step here: run it now, keep its id for the collect
+    int32_t tok = 0;
+    GG_TRY(step_impl(c, token < 0 ? c->last_tok : token, pos, s, u, &tok));
+    c->pipe_tok[slot] = tok;
+    c->pipe_launched[slot] = false;
+  }
+  c->have_prev = true;
+  c->pipe_n += 1;
+  return GG_OK;
+}
+
+int gg_step_collect(gg_ctx* c, int32_t* out_token) {
+  GG_TRY(check_ready(c));
+  if (!out_token) return set_err(c, GG_ERR_INVALID, "null argument");
+  if (c->pipe_n == 0) return set_err(c, GG_ERR_INVALID, "no step outstanding");
+  const int slot = c->pipe_head;
+  c->pipe_head ^= 1;
+  c->pipe_n -= 1;
+  if (c->pipe_launched[slot]) {
+    GG_HIP(c, hipEventSynchronize(c->pipe_ev[slot]));
+    GG_TRY(check_fused(c));
+    *out_token = c->h_out[4 + slot];
+    if (c->pipe_n == 0) c->last_tok = *out_token;
+  } else {
+    *out_token = c->pipe_tok[slot];
+  }
+  return GG_OK;
 }
 
 int gg_penalty_reset(gg_ctx* c) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   GG_HIP(c, hipMemsetAsync(c->seen, 0, (size_t)cdiv(c->V, 32) * 4, c->stream));
   GG_HIP(c, hipMemsetAsync((char*)c->st + offsetof(DevState, seen_count), 0, 4, c->stream));
   return sync(c, "penalty reset");
 }
 
 int gg_penalty_add(gg_ctx* c, const int32_t* ids, int32_t n) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   if (n < 0 || n > c->CTX || (n > 0 && !ids)) return set_err(c, GG_ERR_INVALID, "bad id list");
   if (n == 0) return GG_OK;
   for (int i = 0; i < n; ++i) c->h_tokens[i] = ids[i];
@@ -1190,7 +1275,7 @@ int gg_penalty_add(gg_ctx* c, const int32_t* ids, int32_t n) {
 }
 
 int gg_reset_kv(gg_ctx* c) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   const size_t kvb = (size_t)c->CTX * kHeadDim * 4;
   for (Layer& Ly : c->layers) {
     GG_HIP(c, hipMemsetAsync(Ly.kc, 0, kvb, c->stream));
@@ -1200,7 +1285,7 @@ int gg_reset_kv(gg_ctx* c) {
 }
 
 int gg_read(gg_ctx* c, int32_t what, int32_t layer, void* dst, size_t nbytes) {
-  GG_TRY(check_ready(c));
+  GG_TRY(check_idle(c));
   if (!dst) return set_err(c, GG_ERR_INVALID, "null destination");
   const void* src = nullptr;
   size_t sz = 0;
@@ -1326,6 +1411,8 @@ void gg_destroy(gg_ctx* c) {
   for (hipEvent_t e : c->ev)
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->probe_ev)
+    if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->pipe_ev)
     if (e) (void)hipEventDestroy(e);
   for (void* p : c->allocs) (void)hipFree(p);
   if (c->staging) (void)hipFree(c->staging);

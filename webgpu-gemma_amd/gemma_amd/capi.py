@@ -93,6 +93,8 @@ _SIGS = {
     "gg_select": (ctypes.c_int, [_P, ctypes.POINTER(GGSample), ctypes.c_double, ctypes.POINTER(ctypes.c_int32)]),
     "gg_step": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(GGSample), ctypes.c_double,
                                ctypes.POINTER(ctypes.c_int32)]),
+    "gg_step_submit": (ctypes.c_int, [_P, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(GGSample), ctypes.c_double]),
+    "gg_step_collect": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int32)]),
     "gg_penalty_reset": (ctypes.c_int, [_P]),
     "gg_penalty_add": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int32]),
     "gg_reset_kv": (ctypes.c_int, [_P]),
@@ -207,6 +209,17 @@ class Engine:
         s = sample(temperature, top_p, rep_penalty)
         _check(self.ctx, lib().gg_step(self.ctx, int(token), int(pos), ctypes.byref(s), float(u),
                                        ctypes.byref(out)))
+        return out.value
+
+    def step_submit(self, token: int, pos: int, temperature=0.0, top_p=0.9, rep_penalty=1.0, u=0.0):
+        """Queue a step (token < 0: the id the previous step selects, on the device)."""
+        s = sample(temperature, top_p, rep_penalty)
+        _check(self.ctx, lib().gg_step_submit(self.ctx, int(token), int(pos), ctypes.byref(s), float(u)))
+
+    def step_collect(self) -> int:
+        """Wait for the oldest submitted step and return its id."""
+        out = ctypes.c_int32(-1)
+        _check(self.ctx, lib().gg_step_collect(self.ctx, ctypes.byref(out)))
         return out.value
 
     def penalty_reset(self):

@@ -195,24 +195,67 @@ class GemmaEngineImpl {
     const endCall = this.tokenizer.funcTokens['<end_function_call>'];
     const generated = [next];
     let writes = 0;
+    const isStop = (t) => t === 1 || t === 0 || t === 106;
     yield this.tokenizer.decodeToken(next);
 
-    for (let step = 1; step < maxTokens; step++) {
-      if (next === 1 || next === 0 || next === 106) break;
-      if (endCall !== undefined && next === endCall) break;
-      if (signal && signal.aborted) break;
-      const pos = this.kvPosition + writes;
-      if (pos >= this.config.context_length - 1) break;
-      const tok = next;
-      next = await this.callAsync(() => this.gg.step(this.ctx, tok, pos, temperature, topP, repPenalty, draw()));
-      writes++;
-      if (next === 1 || next === 0 || next === 106) break;
-      if (endCall !== undefined && next === endCall) {
-        generated.push(next);
-        break;
+    if (typeof this.gg.stepSubmit === 'function' && typeof this.gg.stepCollect === 'function') {
+      // The same loop with one step queued ahead: step k + 1 is submitted
+      // before step k's id reaches the host (it takes that id on the device),
+      // so the GPU runs the steps back to back. The ids, the yields and the
+      // stop rules are those of the loop below; a step queued past the end is
+      // collected and dropped (its K/V row lies beyond kvPosition, its id in
+      // the turn's penalty set, which the next turn resets). When sampling, that
+      // dropped step has taken one draw.
+      let inflight = 0;
+      const canStep = (step, pos) =>
+        step < maxTokens && pos < this.config.context_length - 1 && !(signal && signal.aborted);
+      try {
+        if (!isStop(next) && !(endCall !== undefined && next === endCall) && canStep(1, this.kvPosition)) {
+          this.call(() => this.gg.stepSubmit(this.ctx, next, this.kvPosition, temperature, topP, repPenalty, draw()));
+          inflight = 1;
+          for (let step = 1; inflight > 0; step++) {
+            const ahead = this.kvPosition + writes + 1;
+            if (canStep(step + 1, ahead)) {
+              this.call(() => this.gg.stepSubmit(this.ctx, -1, ahead, temperature, topP, repPenalty, draw()));
+              inflight++;
+            }
+            next = await this.callAsync(() => this.gg.stepCollect(this.ctx));
+            inflight--;
+            writes++;
+            if (isStop(next)) break;
+            if (endCall !== undefined && next === endCall) {
+              generated.push(next);
+              break;
+            }
+            generated.push(next);
+            yield this.tokenizer.decodeToken(next);
+            if (signal && signal.aborted) break;
+          }
+        }
+      } finally {
+        while (inflight > 0 && this.ctx) {
+          inflight--;
+          await this.callAsync(() => this.gg.stepCollect(this.ctx));
+        }
       }
-      generated.push(next);
-      yield this.tokenizer.decodeToken(next);
+    } else {
+      for (let step = 1; step < maxTokens; step++) {
+        if (isStop(next)) break;
+        if (endCall !== undefined && next === endCall) break;
+        if (signal && signal.aborted) break;
+        const pos = this.kvPosition + writes;
+        if (pos >= this.config.context_length - 1) break;
+        const tok = next;
+        next = await this.callAsync(() => this.gg.step(this.ctx, tok, pos, temperature, topP, repPenalty, draw()));
+        writes++;
+        if (isStop(next)) break;
+        if (endCall !== undefined && next === endCall) {
+          generated.push(next);
+          break;
+        }
+        generated.push(next);
+        yield this.tokenizer.decodeToken(next);
+      }
     }
     this.conversationHistory.push({ role: 'model', text: this.tokenizer.decodeTokens(generated) });
     this.kvPosition += writes;

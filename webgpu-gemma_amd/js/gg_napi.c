@@ -9,6 +9,9 @@
  *   prefill(ctx, ids, startPos)          prefillBatched            -> Promise
  *   select(ctx, T, topP, rep, u)         getFirstTokenAfterPrefill -> Promise<id>
  *   step(ctx, id, pos, T, topP, rep, u)  forwardPassAndGetToken    -> Promise<id>
+ *   stepSubmit(ctx, id, pos, T, topP, rep, u), stepCollect(ctx) -> Promise<id>
+ *                                        the same step queued ahead (id -1:
+ *                                        the previous step's, on the device)
  *   penaltyReset(ctx), penaltyAdd(ctx, ids)   the per-turn Set(allTokens)
  *   resetKV(ctx)                         resetKVCaches
  *   read(ctx, what, layer, typedArray)   debug readbacks
@@ -319,8 +322,30 @@ static napi_value Destroy(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
-/* ---- asynchronous calls (prefill / select / step) ----------------------- */
-enum { OP_PREFILL, OP_SELECT, OP_STEP };
+/* stepSubmit(ctx, id, pos, T, topP, rep, u): queues a step and returns
+ * without waiting (gg_step_submit); stepCollect awaits it. */
+static napi_value StepSubmit(napi_env env, napi_callback_info info) {
+  napi_value argv[7];
+  if (!get_args(env, info, 7, argv)) return NULL;
+  gg_ctx* ctx = get_ctx(env, argv[0]);
+  if (!ctx) return NULL;
+  int32_t token = 0, pos = 0;
+  gg_sample s;
+  double u = 0.0;
+  if (napi_get_value_int32(env, argv[1], &token) != napi_ok || napi_get_value_int32(env, argv[2], &pos) != napi_ok ||
+      napi_get_value_double(env, argv[3], &s.temperature) != napi_ok ||
+      napi_get_value_double(env, argv[4], &s.top_p) != napi_ok ||
+      napi_get_value_double(env, argv[5], &s.rep_penalty) != napi_ok || napi_get_value_double(env, argv[6], &u) != napi_ok) {
+    napi_throw_type_error(env, "GG_ERR_INVALID", "step arguments must be numbers");
+    return NULL;
+  }
+  int rc = gg_step_submit(ctx, token, pos, &s, u);
+  if (rc != GG_OK) return throw_rc(env, ctx, rc);
+  return NULL;
+}
+
+/* ---- asynchronous calls (prefill / select / step / stepCollect) --------- */
+enum { OP_PREFILL, OP_SELECT, OP_STEP, OP_COLLECT };
 typedef struct {
   int op;
   handle_t* h;
@@ -344,6 +369,7 @@ static void job_execute(napi_env env, void* data) {
     case OP_PREFILL: j->rc = gg_prefill(j->ctx, j->ids, (int32_t)j->n, j->pos); break;
     case OP_SELECT: j->rc = gg_select(j->ctx, &j->s, j->u, &j->out); break;
     case OP_STEP: j->rc = gg_step(j->ctx, j->token, j->pos, &j->s, j->u, &j->out); break;
+    case OP_COLLECT: j->rc = gg_step_collect(j->ctx, &j->out); break;
   }
   if (j->rc != GG_OK) {
     const char* m = gg_last_error(j->ctx);
@@ -471,12 +497,27 @@ static napi_value Step(napi_env env, napi_callback_info info) {
   return queue_job(env, h, j);
 }
 
+static napi_value StepCollect(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  handle_t* h = get_handle(env, argv[0]);
+  if (!h) return NULL;
+  job_t* j = (job_t*)calloc(1, sizeof(job_t));
+  if (!j) {
+    napi_throw_error(env, "GG_ERR_OOM", "host allocation failed");
+    return NULL;
+  }
+  j->op = OP_COLLECT;
+  return queue_job(env, h, j);
+}
+
 static napi_value Init(napi_env env, napi_value exports) {
   struct {
     const char* name;
     napi_callback cb;
   } fns[] = {{"create", Create},   {"upload", Upload},         {"finalize", Finalize}, {"prefill", Prefill},
-             {"select", Select},   {"step", Step},             {"penaltyReset", PenaltyReset},
+             {"select", Select},   {"step", Step},             {"stepSubmit", StepSubmit},
+             {"stepCollect", StepCollect}, {"penaltyReset", PenaltyReset},
              {"penaltyAdd", PenaltyAdd}, {"resetKV", ResetKV}, {"read", Read},         {"destroy", Destroy}};
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
     napi_value f;
