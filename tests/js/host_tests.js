@@ -339,6 +339,24 @@ async function engineTests() {
     }
     assert.ok(dropped > 0);   // the queued-ahead path ran and dropped its extra steps
   });
+  await test('engine: a generator left unfinished has its queued step collected before the next call', async () => {
+    const gg = new PipeGG([215, 216], () => 211);
+    const e = await createGemmaEngine({ model: ggufPath, backend: gg, contextLength: 64 });
+    e.addUserMessage('Hello');
+    const it = e.generate({ temperature: 0 });
+    await it.next();
+    await it.next();                   // a step is queued; the generator is then abandoned
+    assert.strictEqual(gg.queue.length, 1);
+    e.resetConversation();             // the KV reset waits for the queued step
+    assert.strictEqual(gg.calls.filter((c) => c[0] === 'resetKV').length, 0);
+    e.addUserMessage('the');
+    const out = await collect(e.generate({ temperature: 0, maxTokens: 3 }));
+    assert.strictEqual(out.length, 3);
+    assert.strictEqual(gg.queue.length, 0);
+    assert.strictEqual(gg.calls.filter((c) => c[0] === 'resetKV').length, 1);
+    const pfs = gg.calls.filter((c) => c[0] === 'prefill');
+    assert.strictEqual(pfs[1][2], 0);  // a fresh conversation from position 0
+  });
   await test('engine: context overflow resets the KV cache and keeps only the last user message', async () => {
     const { e, gg } = await mk([210, 106, 210, 106]);
     e.addUserMessage('Hello');

@@ -69,6 +69,8 @@ class GemmaEngineImpl {
     this.conversationHistory = [];
     this.kvPosition = 0;
     this.deviceLost = false;
+    this.inflight = 0;          // steps queued ahead and not yet collected
+    this.resetPending = false;  // resetConversation() while a step was queued
   }
 
   reportProgress(loaded, total, status) {
@@ -165,6 +167,12 @@ class GemmaEngineImpl {
     const maxTokens = o.maxTokens === undefined ? 32768 : o.maxTokens;
     const toolsJson = o.toolsJson === undefined ? '[]' : o.toolsJson;
     const signal = o.signal;
+    // a previous generator left unfinished may still have a step queued
+    await this.drain();
+    if (this.resetPending) {
+      this.resetPending = false;
+      this.call(() => this.gg.resetKV(this.ctx));
+    }
     // the uniform draw is taken only when sampling (engine.ts:878,894)
     const draw = () => (temperature === 0 ? 0 : this.random());
 
@@ -206,21 +214,20 @@ class GemmaEngineImpl {
       // collected and dropped (its K/V row lies beyond kvPosition, its id in
       // the turn's penalty set, which the next turn resets). When sampling, that
       // dropped step has taken one draw.
-      let inflight = 0;
       const canStep = (step, pos) =>
         step < maxTokens && pos < this.config.context_length - 1 && !(signal && signal.aborted);
       try {
         if (!isStop(next) && !(endCall !== undefined && next === endCall) && canStep(1, this.kvPosition)) {
           this.call(() => this.gg.stepSubmit(this.ctx, next, this.kvPosition, temperature, topP, repPenalty, draw()));
-          inflight = 1;
-          for (let step = 1; inflight > 0; step++) {
+          this.inflight = 1;
+          for (let step = 1; this.inflight > 0; step++) {
             const ahead = this.kvPosition + writes + 1;
             if (canStep(step + 1, ahead)) {
               this.call(() => this.gg.stepSubmit(this.ctx, -1, ahead, temperature, topP, repPenalty, draw()));
-              inflight++;
+              this.inflight++;
             }
             next = await this.callAsync(() => this.gg.stepCollect(this.ctx));
-            inflight--;
+            this.inflight--;
             writes++;
             if (isStop(next)) break;
             if (endCall !== undefined && next === endCall) {
@@ -233,10 +240,7 @@ class GemmaEngineImpl {
           }
         }
       } finally {
-        while (inflight > 0 && this.ctx) {
-          inflight--;
-          await this.callAsync(() => this.gg.stepCollect(this.ctx));
-        }
+        await this.drain();
       }
     } else {
       for (let step = 1; step < maxTokens; step++) {
@@ -261,10 +265,23 @@ class GemmaEngineImpl {
     this.kvPosition += writes;
   }
 
+  // Collects (and drops) any step still queued by a generator that was left
+  // unfinished without being returned.
+  async drain() {
+    while (this.inflight > 0 && this.ctx) {
+      this.inflight--;
+      await this.callAsync(() => this.gg.stepCollect(this.ctx));
+    }
+    this.inflight = 0;
+  }
+
   resetConversation() {
     this.conversationHistory = [];
     this.kvPosition = 0;
-    if (this.ctx) this.call(() => this.gg.resetKV(this.ctx));
+    if (!this.ctx) return;
+    // with a step still queued the KV reset waits for the next generate()
+    if (this.inflight > 0) this.resetPending = true;
+    else this.call(() => this.gg.resetKV(this.ctx));
   }
 
   dispose() {
