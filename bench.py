@@ -250,7 +250,10 @@ def main():
         copy_calibration(args.copy_calibration)
     # positions decoded past the context: the timed engine's warm-up, timed and
     # device-timing steps, or the kernel-timing engine's 4 + probe_steps
-    ctx_len = max(4096, args.ctx + max(args.warmup + args.steps + min(args.steps, 64), 4 + args.probe_steps) + 8)
+    # positions used after the prompt: warm-up, the timed steps and the one
+    # queued past them, the synchronous reference loop, the event-timed loop
+    after = args.warmup + args.steps + 1 + min(args.steps, 128) + min(args.steps, 64)
+    ctx_len = max(4096, args.ctx + max(after, 4 + args.probe_steps) + 8)
     shape = synth.GEMMA3_1B.with_ctx(ctx_len)
     shape = shape.reference_mode() if args.reference_mode else shape.gemma3_mode()
     t0 = time.perf_counter()

@@ -1125,6 +1125,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
         // long span: every block takes a chunk of the four heads
         if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
+        stamp(a, b, l, 14);
       } else if (Ly.window == 0 && b < 64) {
         // full-attention layers: blocks [0, 64) also take chunks 16..31
         const int c = 16 + (b & 7) + 8 * (b >> 5), h = (b >> 3) & 3;
