@@ -227,6 +227,11 @@ async function engineTests() {
       fs.rmdirSync(dir);
     }
   });
+  await test('engine: batched MFMA prefill by default; a negative prefillBatch keeps the token-by-token order', async () => {
+    assert.strictEqual((await mk([])).gg.calls[0][1].prefill_batch, 64);   // whole prompt, capped by the context
+    assert.strictEqual((await mk([], { prefillBatch: 48 })).gg.calls[0][1].prefill_batch, 48);
+    assert.strictEqual((await mk([], { prefillBatch: -1 })).gg.calls[0][1].prefill_batch, 0);
+  });
   await test('engine: create() gets the file\'s rope bases (one base in reference mode)', async () => {
     const ref = (await mk([])).gg.calls[0][1];
     assert.strictEqual(ref.rope_theta_global, expect.rope_base);

@@ -40,7 +40,8 @@ def test_js_host_on_gpu(gpu, tmp_path, attention):
     run_shape = shape.gemma3_mode(window=512) if attention == "gemma3" else shape.reference_mode()
 
     # replay the same calls through the Python binding of the C-ABI
-    e = capi.Engine(run_shape.gg_config())
+    # the host's default: the batched MFMA prefill, the whole prompt per slice
+    e = capi.Engine(run_shape.gg_config(prefill_batch=min(4096, run_shape.ctx)))
     e.upload_model(tensors)
     e.finalize()
     for c in log:

@@ -64,6 +64,9 @@ class GemmaEngineImpl {
     // 'reference' (one theta, full attention: src/ as shipped) or 'gemma3'
     // (local layers: theta 1e4, 512-position window)
     this.attention = options.attention || 'reference';
+    // rows per batched MFMA prefill slice: unset or 0 = the whole prompt
+    // (at most 4096 rows per slice); a negative value keeps the reference's
+    // token-by-token prefill (engine.ts:923-928)
     this.prefillBatch = options.prefillBatch || 0;
     this.ctx = null;
     this.conversationHistory = [];
@@ -110,7 +113,8 @@ class GemmaEngineImpl {
         rope_theta_global: cfg.rope_theta_global, rope_theta_local: cfg.rope_theta_swa,
         swa_period: cfg.swa_period, sliding_window: cfg.sliding_window,
         attention_mode: this.attention === 'gemma3' ? GG_ATTN_GEMMA3 : GG_ATTN_REFERENCE,
-        prefill_batch: this.prefillBatch,
+        prefill_batch: this.prefillBatch < 0 ? 0
+          : this.prefillBatch > 0 ? this.prefillBatch : Math.min(4096, cfg.context_length),
       }));
       const total = g.tensors.reduce((a, t) => a + gguf.tensorByteSize(t), 0);
       let loaded = 0;

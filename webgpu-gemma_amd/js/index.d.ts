@@ -50,7 +50,10 @@ export interface GemmaEngineOptions {
    * the file's sliding-window base) and a 512-position window.
    */
   attention?: 'reference' | 'gemma3';
-  /** Rows per batched prefill slice (0: whole prompt, at most 4096). */
+  /**
+   * Rows per batched MFMA prefill slice. Unset or 0: the whole prompt (at most
+   * 4096 rows per slice). Negative: the reference's token-by-token prefill.
+   */
   prefillBatch?: number;
   /** Directory holding gg_napi.node and libgg.so (default: ../lib beside this file). */
   bindingDir?: string;
