@@ -20,12 +20,22 @@ class Tokenizer {
     this.vocab = vocab;
     this.idOf = new Map();
     this.maxLen = 0;
+    // the lengths of the entries that start with each first code unit,
+    // longest first: only those can match there, so the longest match is
+    // found with a lookup per such length instead of one per length up to
+    // maxLen (same result)
+    const lens = new Map();
     for (let i = 0; i < vocab.length; i++) {
       const t = vocab[i];
       if (!t) continue;
       if (!this.idOf.has(t)) this.idOf.set(t, i);
       if (t.length > this.maxLen) this.maxLen = t.length;
+      const l = lens.get(t[0]);
+      if (l) l.add(t.length);
+      else lens.set(t[0], new Set([t.length]));
     }
+    this.lensByFirst = new Map();
+    for (const [c, l] of lens) this.lensByFirst.set(c, Array.from(l).sort((a, b) => b - a));
     this.special = Object.assign({}, SPECIALS);
     this.funcTokens = {};
     for (const name of FUNCTION_TOKENS) {
@@ -47,24 +57,30 @@ class Tokenizer {
   }
 
   encodeSegment(text, prefix) {
-    let rest = (prefix ? SPACE : '') + text.replace(/ /g, SPACE);
+    const str = (prefix ? SPACE : '') + text.replace(/ /g, SPACE);
     const out = [];
-    while (rest.length > 0) {
+    let pos = 0;
+    while (pos < str.length) {
       let hit = -1;
       let hitLen = 0;
-      for (let len = Math.min(rest.length, this.maxLen); len >= 1; len--) {
-        const id = this.idOf.get(rest.substring(0, len));
-        if (id !== undefined) {
-          hit = id;
-          hitLen = len;
-          break;
+      const lens = this.lensByFirst.get(str[pos]);
+      if (lens) {
+        const left = str.length - pos;
+        for (const len of lens) {
+          if (len > left) continue;
+          const id = this.idOf.get(str.substring(pos, pos + len));
+          if (id !== undefined) {
+            hit = id;
+            hitLen = len;
+            break;
+          }
         }
       }
       if (hitLen === 0) {
-        rest = rest.slice(1);   // no vocabulary entry starts here: drop one character
+        pos += 1;   // no vocabulary entry starts here: drop one character
       } else {
         out.push(hit);
-        rest = rest.slice(hitLen);
+        pos += hitLen;
       }
     }
     return out;
