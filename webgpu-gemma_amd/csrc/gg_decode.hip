@@ -38,7 +38,11 @@
 // DEC_STEP: every block takes one vocabulary class c (rows c + 256 k, the
 // stride classes of argmax / topk256, shaders.ts:327-384) of the tied LM
 // head, from a class-major copy of the embedding, and hands over its
-// class candidate; block 0 selects the token (engine.ts:805-902).
+// class candidate; block 0 selects the token (engine.ts:805-902): the
+// halving tree in the SAMPLE = false copy that greedy steps launch, the
+// sampler in the SAMPLE = true copy. A step whose token argument is negative
+// embeds the id the previous launch selected (DevState::out_token), so the
+// host can queue the next step before that id reaches it.
 //
 // Every wait is bounded (a.spin_limit ticks of s_memrealtime): a block that
 // times out raises the host-visible flag and leaves, so the launch always
