@@ -1,6 +1,6 @@
 'use strict';
 // Context lifetime of the Node-API binding (gg_napi.c) over a stub libgg
-// whose prefill/select/step sleep: a second job on a busy context is refused
+// whose prefill/select/step/stepCollect sleep: a second job on a busy context is refused
 // with GG_ERR_INVALID, destroy() during a step is deferred until the step's
 // completion, calls on a destroyed context are refused, and a context whose
 // JavaScript handle is garbage-collected during a step is destroyed after it.
@@ -66,6 +66,21 @@ async function main() {
     await tick();
   }
   console.log('ok gc mid-step');
+
+  // pipelined steps: stepSubmit is synchronous, stepCollect a job (the context
+  // is busy until it completes), destroy() during a collect is deferred
+  const d = gg.create({ hidden_size: 8 });
+  gg.stepSubmit(d, 5, 0, 0, 1, 1, 0.5);
+  const p5 = gg.stepCollect(d);
+  expectCode(() => gg.stepSubmit(d, -1, 1, 0, 1, 1, 0.5), 'GG_ERR_INVALID', 'submit while a collect runs');
+  if ((await p5) !== 6) throw new Error('collected id');
+  gg.stepSubmit(d, -1, 1, 0, 1, 1, 0.5);
+  const p6 = gg.stepCollect(d);
+  await sleep(50);
+  gg.destroy(d);
+  if ((await p6) !== 7) throw new Error('collected id after destroy');
+  expectCode(() => gg.stepSubmit(d, 1, 2, 0, 1, 1, 0.5), 'GG_ERR_INVALID', 'submit after destroy');
+  console.log('ok pipelined steps');
   console.log('lifecycle passed');
 }
 

@@ -42,6 +42,9 @@ def check_log(stderr):
     assert per["2"] == ["create", "prefill", "prefill-end", "destroy"], per
     # context 3: a step; if the collector finalized the handle, destroy comes after the step
     assert per["3"][:3] == ["create", "step", "step-end"] and per["3"][3:] in ([], ["destroy"]), per
+    # context 4: pipelined steps, destroyed after the second collect ended
+    assert per["4"] == ["create", "step_submit", "step_submit-end", "step_collect", "step_collect-end",
+                        "step_submit", "step_submit-end", "step_collect", "step_collect-end", "destroy"], per
 
 
 @pytest.mark.skipif(NODE is None or not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")),
