@@ -98,6 +98,7 @@ __device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag
   const char* sb = (const char*)src;
   const long long t0 = __builtin_amdgcn_s_memrealtime();
   for (;;) {
+    const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
     uint64_t w[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) w[k] = ll_ld((const uint64_t*)(sb + (uint32_t)(8 * (tid + NT * k))));
@@ -109,7 +110,7 @@ __device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag
       for (int k = 0; k < PER; ++k) v[k] = ll_val(w[k]);
       return true;
     }
-    if (__builtin_amdgcn_s_memrealtime() - t0 > limit) return false;
+    if (now_ - t0 > limit) return false;
   }
 }
 
@@ -528,6 +529,7 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
     const uint64_t* src = a.x_qkv + (wv == 0 ? h * kHeadDim : a.QD + (wv - 1) * kHeadDim);
     const long long st0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
+      const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
       uint64_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = ll_ld(src + (wv == 2 ? 4 * lane + i : lane + 64 * i));
@@ -539,7 +541,7 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
         for (int i = 0; i < 4; ++i) hx[i] = ll_val(w[i]);
         break;
       }
-      if (__builtin_amdgcn_s_memrealtime() - st0 > lim) { ok = false; break; }
+      if (now_ - st0 > lim) { ok = false; break; }
     }
   }
   // QK-norm + NEOX RoPE (fusedPerHeadNormRope): lane owns dims lane + 64 i
@@ -667,6 +669,7 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
   if (tid < kHeadDim) {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
+      const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
       uint64_t wo[NC];
 #pragma unroll
       for (int c = 0; c < NC; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
@@ -681,7 +684,7 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
         if (tid < 2 * NC) S.red[0][tid] = ll_val(ws);
         break;
       }
-      if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_limit) { ok = false; break; }
+      if (now_ - t0 > a.spin_limit) { ok = false; break; }
     }
   }
   if (failed(S, ok)) return false;
@@ -815,6 +818,7 @@ __device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, con
   {
     const long long st0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
+      const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
       uint64_t w[4], e[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = ll_ld(qsrc + lane + 64 * i);
@@ -837,7 +841,7 @@ __device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, con
         }
         break;
       }
-      if (__builtin_amdgcn_s_memrealtime() - st0 > lim) { ok = false; break; }
+      if (now_ - st0 > lim) { ok = false; break; }
     }
   }
   if (ok) {
@@ -975,6 +979,7 @@ __device__ __forceinline__ bool merge_long(const DecodeArgs& a, Smem& S, int l, 
   {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
+      const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
       uint64_t w[KC];
 #pragma unroll
       for (int k = 0; k < KC; ++k) w[k] = ll_ld(base + (size_t)(g + 16 * k) * kDecPart + 16 * s + d);
@@ -990,7 +995,7 @@ __device__ __forceinline__ bool merge_long(const DecodeArgs& a, Smem& S, int l, 
         lt = ll_val(wl);
         break;
       }
-      if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_limit) { ok = false; break; }
+      if (now_ - t0 > a.spin_limit) { ok = false; break; }
     }
   }
   if (failed(S, ok)) return false;
@@ -1254,6 +1259,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       float acc = 0.f;
       bool ok = true;
       for (;;) {
+        const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
         uint64_t w[PR];
 #pragma unroll
         for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + 32 * k, a.g_f - 1) * H);
@@ -1266,7 +1272,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
             if (mt + 32 * k < a.g_f) acc += ll_val(w[k]);
           break;
         }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
+        if (now_ - t0 > lim) { ok = false; break; }
       }
       soft_fail(S, ok);
       stamp(a, b, l, 7);
@@ -1424,13 +1430,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   if (tid < 256) {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
+      const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
       const uint64_t wv0 = ll_ld(a.x_cand + 2 * tid), wi0 = ll_ld(a.x_cand + 2 * tid + 1);
       if (ll_ok(wv0, tagC) & ll_ok(wi0, tagC)) {
         m = ll_val(wv0);
         id = __float_as_uint(ll_val(wi0));
         break;
       }
-      if (__builtin_amdgcn_s_memrealtime() - t0 > lim) { ok = false; break; }
+      if (now_ - t0 > lim) { ok = false; break; }
     }
   }
   if (failed(S, ok)) { report_timeout(a); return; }
