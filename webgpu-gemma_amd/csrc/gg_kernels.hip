@@ -1224,8 +1224,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
   const int M = a.M, K = a.K;
-  // Tile order: block b (launch order) runs on XCD b % 8, and XCD x takes the
-  // contiguous range [x G / 8, (x + 1) G / 8) of an order with the K slice
+  // Tile order: workgroups go to the XCDs round-robin (from an XCD that
+  // depends on earlier dispatches), so the blocks with one value of b % 8
+  // (launch order) share an XCD; they take the contiguous range
+  // [(b % 8) G / 8, (b % 8 + 1) G / 8) of an order with the K slice
   // slowest, then groups of 4 tile rows with the rows fastest, so that the
   // blocks sharing an XCD's L2 share A rows and W tiles (fewer L2 misses).
   const int NT = gridDim.x, MT = gridDim.y, G = NT * MT * gridDim.z;
