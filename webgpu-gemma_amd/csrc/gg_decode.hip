@@ -416,14 +416,21 @@ __device__ __forceinline__ float gate_up_mfma(const Smem& S, const i32x4* wb, co
   const int as = valid ? 192 : 0;
   const float* sc = (const float*)S.xsc4[hb];
   const i32x4 zero = {0, 0, 0, 0};
-  float acc = 0.f;
+  // all products first, each into its own accumulator, so that the MFMAs
+  // issue back to back instead of each waiting for the previous result to be
+  // read out; then the f32 sums in increasing c
+  i32x4 C[kMaxKq];
 #pragma unroll
   for (int c = 0; c < kMaxKq; ++c) {
     const i32x4 A = *(const i32x4*)(ab + c * as);
-    const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, wb[c], zero, 0, 0, 0);
+    C[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, wb[c], zero, 0, 0, 0);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxKq; ++c) {
     const uint32_t w2 = wsc[c >> 1];
     const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? w2 >> 16 : w2 & 0xffffu));
-    acc = fmaf(planes_value(C[0], C[1], C[2]), sc[c] * d, acc);
+    acc = fmaf(planes_value(C[c][0], C[c][1], C[c][2]), sc[c] * d, acc);
   }
   return acc;
 }
