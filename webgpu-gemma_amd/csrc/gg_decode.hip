@@ -23,8 +23,9 @@
 //       query head), 16 chunks per head in sliding-window layers, 32 in
 //       full-attention layers with blocks [0, 64) taking chunks 16..31 after
 //       their QKV rows (fusedPerHeadNormRope, kvCacheStore,
-//       attnScore/softmax/attnOutput, shaders.ts:209-325); chunk 0's block
-//       of each head merges the head's chunk partials. Full-attention
+//       attnScore/softmax/attnOutput, shaders.ts:209-325); the blocks of
+//       chunks 0..3 of each head merge the head's chunk partials, 64 dims
+//       each. Full-attention
 //       layers at spans above 4096 positions (k_decode<MODE, true>, for
 //       contexts above 4096): every block takes one of 256 chunks for all
 //       four heads (each K/V row read once), blocks [192, 256) merge.
@@ -663,31 +664,37 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
   return true;
 }
 
-// Chunk 0's block of head h: merge the head's NC chunk partials,
+// Chunk block p < 4 of head h: dims 64 p .. 64 p + 63 of the head's merge,
 // o = sum_c f_c o_c / sum_c f_c l_c with f_c = 2^(m_c - max m) (maxima in
-// log2 units; empty chunks have m_c = -inf), into the O GEMV's input.
-// Threads 0..2 NC - 1 poll the (m, l) words, threads 0..255 one dim of each o_c.
+// log2 units; empty chunks have m_c = -inf), into the O GEMV's input (the
+// four quarters run in four blocks, each polling a quarter of the partial
+// words). Wave g polls dim 64 p + lane of chunks g, g + 4, ...;
+// threads 0..2 NC - 1 also poll the (m, l) words. Every thread forms the
+// head's max and l-sum in chunk order; wave g sums its chunks in order and
+// the four waves' sums are added in wave order.
 template <int NC>
-__device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, int h, uint32_t tag) {
-  const int tid = tidx();
+__device__ __forceinline__ bool merge_head_part(const DecodeArgs& a, Smem& S, int l, int h, int p, uint32_t tag) {
+  constexpr int KC = NC / 4;
+  const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
   const uint64_t* base = a.x_part + (size_t)h * kDecChunksG * kDecPart;
+  const int d = 64 * p + lane;
   bool ok = true;
-  float oc[NC];
-  if (tid < kHeadDim) {
+  float oc[KC];
+  {
     const long long t0 = __builtin_amdgcn_s_memrealtime();
     for (;;) {
       const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
-      uint64_t wo[NC];
+      uint64_t wo[KC];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) wo[c] = ll_ld(base + c * kDecPart + tid);
+      for (int k = 0; k < KC; ++k) wo[k] = ll_ld(base + (wv + 4 * k) * kDecPart + d);
       const int si = min(tid, 2 * NC - 1);   // (m, l) word of threads < 2 NC
       const uint64_t ws = ll_ld(base + (si >> 1) * kDecPart + kHeadDim + (si & 1));
       bool good = (tid >= 2 * NC) | ll_ok(ws, tag);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) good &= ll_ok(wo[c], tag);
+      for (int k = 0; k < KC; ++k) good &= ll_ok(wo[k], tag);
       if (good) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) oc[c] = ll_val(wo[c]);
+        for (int k = 0; k < KC; ++k) oc[k] = ll_val(wo[k]);
         if (tid < 2 * NC) S.red[0][tid] = ll_val(ws);
         break;
       }
@@ -696,20 +703,20 @@ __device__ __forceinline__ bool merge_head(const DecodeArgs& a, Smem& S, int l, 
   }
   if (failed(S, ok)) return false;
   stamp(a, blockIdx.x, l, 13);
-  if (tid < kHeadDim) {
-    float M = -INFINITY;
+  float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) M = fmaxf(M, S.red[0][2 * c]);
-    float L = 0.f, acc = 0.f;
+  for (int c = 0; c < NC; ++c) M = fmaxf(M, S.red[0][2 * c]);
+  float L = 0.f, acc = 0.f;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float f = __builtin_amdgcn_exp2f(S.red[0][2 * c] - M);
-      L = fmaf(f, S.red[0][2 * c + 1], L);
-      acc = fmaf(f, oc[c], acc);
-    }
-    const float x = acc * (1.f / L);
-    ll_st(a.x_attn + h * kHeadDim + tid, x, tag);
-    if (l == a.L - 1) a.attn_out[h * kHeadDim + tid] = x;
+  for (int c = 0; c < NC; ++c) L = fmaf(__builtin_amdgcn_exp2f(S.red[0][2 * c] - M), S.red[0][2 * c + 1], L);
+#pragma unroll
+  for (int k = 0; k < KC; ++k) acc = fmaf(__builtin_amdgcn_exp2f(S.red[0][2 * (wv + 4 * k)] - M), oc[k], acc);
+  if (wv > 0) S.red[wv][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+    const float x = (((acc + S.red[1][lane]) + S.red[2][lane]) + S.red[3][lane]) * (1.f / L);
+    ll_st(a.x_attn + h * kHeadDim + d, x, tag);
+    if (l == a.L - 1) a.attn_out[h * kHeadDim + d] = x;
   }
   return true;
 }
@@ -1165,8 +1172,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         return;
       }
       stamp(a, b, l, 2);
-      if (c == 0) {
-        const bool mok = glob ? merge_head<kDecChunksG>(a, S, l, h, tag) : merge_head<kDecChunks>(a, S, l, h, tag);
+      if (c < 4) {
+        const bool mok =
+            glob ? merge_head_part<kDecChunksG>(a, S, l, h, c, tag) : merge_head_part<kDecChunks>(a, S, l, h, c, tag);
         if (!mok) { report_timeout(a); return; }
         stamp(a, b, l, 3);
       }
