@@ -576,11 +576,6 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
   }
   if (failed(S, ok)) return false;
   stamp(a, blockIdx.x, l, 12);
-  if (holder && h == 0 && tid < kHeadDim) {
-    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
-    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
-  }
-  if (c == 0 && tid < 64) *(float4*)(a.q_dbg + (size_t)l * a.QD + h * kHeadDim + 4 * tid) = S.qs4[tid];
 
   float4 qr[8];
 #pragma unroll
@@ -661,6 +656,15 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
       ll_st(part + kHeadDim + 1, L, tag);
     }
   }
+  // this token's K/V row and the debug copy of q go out last: a store issued
+  // before the dot products would hold their wait for the K/V loads (the
+  // vector memory counter also counts stores) until it is acknowledged; the
+  // chunks read row pos from LDS, later launches from the cache
+  if (holder && h == 0 && tid < kHeadDim) {
+    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
+    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
+  }
+  if (c == 0 && tid < 64) *(float4*)(a.q_dbg + (size_t)l * a.QD + h * kHeadDim + 4 * tid) = S.qs4[tid];
   return true;
 }
 
@@ -865,11 +869,6 @@ __device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, con
   }
   if (failed(S, ok)) return false;
   stamp(a, blockIdx.x, l, 12);
-  if (holder) {
-    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
-    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
-  }
-  if (c == 0) *(float4*)(a.q_dbg + (size_t)l * a.QD + 4 * tid) = LA.qs[wv][lane];
 
   float4 qr[kAttnMaxQ][8];
 #pragma unroll
@@ -973,6 +972,13 @@ __device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, con
       ll_st(part + kHeadDim + 1, L, tag);
     }
   }
+  // this token's K/V row and the debug copy of q go out last (as in
+  // attention_block)
+  if (holder) {
+    gmem(Ly.kc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.ks4)[tid];
+    gmem(Ly.vc)[(size_t)pos * kHeadDim + tid] = ((const float*)S.vs4)[tid];
+  }
+  if (c == 0) *(float4*)(a.q_dbg + (size_t)l * a.QD + 4 * tid) = LA.qs[wv][lane];
   return true;
 }
 
