@@ -499,27 +499,27 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
   const int kv_last = max(pos - 1, 0);   // cache rows [0, pos) hold earlier tokens
   const int pl = lane >> 3, oc = lane & 7;
   const bool holder = (c == nch - 1);
-  float4 kr[8], vr[8];
-  auto load_k = [&](int p) {
+  float4 kr[8], kn[8], vr[8], vn[8];
+  auto load_k = [&](int p, float4* dst) {
     const int t = min(t0 + 8 * NW * p + 8 * wv + pl, kv_last);
     const GG_GLOBAL f32x4* kp = (const GG_GLOBAL f32x4*)(gmem(Ly.kc) + (size_t)t * kHeadDim);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const f32x4 v = __builtin_nontemporal_load(kp + oc + 8 * j);
-      kr[j] = make_float4(v.x, v.y, v.z, v.w);
+      dst[j] = make_float4(v.x, v.y, v.z, v.w);
     }
   };
-  auto load_v = [&](int p) {
+  auto load_v = [&](int p, float4* dst) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int t = min(t0 + 8 * NW * p + 8 * wv + i, kv_last);
       const f32x4 v = __builtin_nontemporal_load((const GG_GLOBAL f32x4*)(gmem(Ly.vc) + (size_t)t * kHeadDim) + lane);
-      vr[i] = make_float4(v.x, v.y, v.z, v.w);
+      dst[i] = make_float4(v.x, v.y, v.z, v.w);
     }
   };
   // K/V rows of the first pass and the RoPE row go out before the q/k/v poll
-  load_k(0);
-  load_v(0);
+  load_k(0, kr);
+  load_v(0, vr);
   const GG_GLOBAL float* rt = gmem(Ly.rope) + (size_t)pos * kHeadDim;
   float cs[2], sn[2], nw[4];
 #pragma unroll
@@ -586,6 +586,13 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
   for (int p = 0; p < npass; ++p) {
     const int tb = t0 + 8 * NW * p + 8 * wv;
     const int t = tb + pl;
+    // the next pass's K/V rows go out before this pass's products (a second
+    // register set), so a pass after the first waits for less of their
+    // latency
+    if (p + 1 < npass) {
+      load_k(p + 1, kn);
+      load_v(p + 1, vn);
+    }
     if (t == pos) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) kr[j] = S.ks4[oc + 8 * j];
@@ -600,7 +607,8 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
     }
     d = group8_sum(d);
     const float sc = t < t1 ? d * sl2 : -INFINITY;
-    if (p + 1 < npass) load_k(p + 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kr[j] = kn[j];
     const float mx = across8_max(sc);
     const float mn = fmaxf(m, mx);
     const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
@@ -622,7 +630,8 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
       o4.z = fmaf(pv, vr[i].z, o4.z);
       o4.w = fmaf(pv, vr[i].w, o4.w);
     }
-    if (p + 1 < npass) load_v(p + 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = vn[i];
   }
   // merge the eight waves (fixed order) into the chunk's (max, sum, o)
   S.wo[wv][lane] = o4;
