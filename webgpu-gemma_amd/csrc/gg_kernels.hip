@@ -1173,14 +1173,37 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
   pf_tile_span(a, row / kPfRows, &klo, &khi, &nkc);
   if (nkc == 1) return;
   const float* pr = a.part + (size_t)row * kPrefillChunks * nq * (2 + kHeadDim);
+  // chunks in groups of four, each group's loads issued together (clamped
+  // indices; a group's chunks past nkc are skipped in the sums); the sums run
+  // in chunk order
+  constexpr int G = 4;
   float M = -INFINITY;
-  for (int c = 0; c < nkc; ++c) M = fmaxf(M, pr[(c * nq + h) * (2 + kHeadDim)]);
+  for (int c0 = 0; c0 < nkc; c0 += G) {
+    float m[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) m[j] = pr[(min(c0 + j, nkc - 1) * nq + h) * (2 + kHeadDim)];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (c0 + j < nkc) M = fmaxf(M, m[j]);
+  }
   float L = 0.f, O = 0.f;
-  for (int c = 0; c < nkc; ++c) {
-    const float* pc = pr + (c * nq + h) * (2 + kHeadDim);
-    const float f = pc[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pc[0] - M);
-    L = fmaf(f, pc[1], L);
-    O = fmaf(f, pc[2 + tid], O);
+  for (int c0 = 0; c0 < nkc; c0 += G) {
+    float m[G], l[G], o[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float* pc = pr + (min(c0 + j, nkc - 1) * nq + h) * (2 + kHeadDim);
+      m[j] = pc[0];
+      l[j] = pc[1];
+      o[j] = pc[2 + tid];
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (c0 + j < nkc) {
+        const float f = m[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[j] - M);
+        L = fmaf(f, l[j], L);
+        O = fmaf(f, o[j], O);
+      }
+    }
   }
   const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + tid;
   split_bf16(O / L, &a.pf_out[e], &a.pf_out[(size_t)a.pf_rows * nq * kHeadDim + e]);
