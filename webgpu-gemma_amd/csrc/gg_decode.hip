@@ -1132,7 +1132,13 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     };
     if (qb) mg_issue<8, 1>(Ly.qkv, Kq, a.kps_qkv, b * a.kps_qkv, a.kps_qkv, wq);
     if (qb) load_norm(norm_of(a, Ly, 0), H, wn);
-    if (l > 0) {
+    // the previous layer's down output into the residual stream; attention
+    // blocks of the chunk layout without an FFN block defer it until after
+    // their chunk (they need the residual only for the LM head), so they
+    // start their K/V loads and q poll at once and poll x_down when it is
+    // long there
+    const bool defer = !qb && !ffb && !(LONG && Ly.window == 0 && pos >= kDecMaxCtx);
+    auto update_resid = [&]() __attribute__((always_inline)) {
       float dv[kEPT], wpost[kEPT];
       load_norm(norm_of(a, layer_view(a, l - 1), 5), H, wpost);
       const bool ok = ll_wait<kEPT>(a.x_down, H, tag - 1, dv, lim);
@@ -1144,6 +1150,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       } else {
         resid_norm<false>(S, dv, wpost, wn, H, a.eps, r);
       }
+    };
+    if (l > 0 && !defer) {
+      update_resid();
       if (b == 0) {
 #pragma unroll
         for (int i = 0; i < kEPT; ++i)
@@ -1193,6 +1202,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         if (!mok) { report_timeout(a); return; }
         stamp(a, b, l, 3);
       }
+      if (l > 0 && defer) update_resid();
       issue_ffn();
     }
     __syncthreads();
