@@ -17,6 +17,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["gg_kernels.hip", "gg_decode.hip", "gg_runtime.hip"]
+# Per-source scheduler: the persistent decode kernel is one long latency chain
+# at one wave per SIMD; the iterative ILP scheduler measured 1.0% faster per
+# step than the default on it (other strategies: max-ilp +1.2%,
+# max-memory-clause +4.4%, iterative-minreg +15%).
+EXTRA = {"gg_decode.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 
 
 def _run(cmd, cwd=None):
@@ -33,7 +38,8 @@ def build_lib() -> str:
     objs = []
     for s in SOURCES:
         o = os.path.join(LIBDIR, s.replace(".hip", ".o"))
-        _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s), "-o", o])
+        _run([HIPCC, *HIP_FLAGS, *EXTRA.get(s, []), "-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s),
+              "-o", o])
         objs.append(o)
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
