@@ -18,12 +18,15 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["gg_kernels.hip", "gg_decode.hip", "gg_runtime.hip"]
 # Per-source options: the persistent decode kernel is one long latency chain
-# at one wave per SIMD. With -O2 (its loops are unrolled by pragmas) the
-# iterative max-occupancy scheduler measured 0.6% faster per step than the
-# iterative ILP one on two boxes, which was itself 1.0% faster than the default
-# at -O3 (other strategies: max-ilp +1.2%, max-memory-clause +4.4%,
-# iterative-minreg +15%; -O1 +5%). The later -O2 overrides HIP_FLAGS' -O3.
-EXTRA = {"gg_decode.hip": ["-O2", "-mllvm", "-amdgpu-sched-strategy=iterative-maxocc"]}
+# at one wave per SIMD. Per step, on two boxes each:
+# - MFMA results in ordinary VGPRs rather than accumulation registers
+#   (-amdgpu-mfma-vgpr-form): 1.4% faster; no copies out of the accumulators;
+# - the iterative max-occupancy scheduler at -O2: 0.6% faster than iterative
+#   ILP, itself 1.0% faster than the default at -O3 (max-ilp +1.2%,
+#   max-memory-clause +4.4%, iterative-minreg +15%; -O1 +5%).
+# The later -O2 overrides HIP_FLAGS' -O3.
+EXTRA = {"gg_decode.hip": ["-O2", "-mllvm", "-amdgpu-sched-strategy=iterative-maxocc",
+                           "-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _run(cmd, cwd=None):
