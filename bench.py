@@ -108,6 +108,220 @@ def prefill_report(shape, args, prefill_s: float) -> dict:
     return out
 
 
+class Hip:
+    """The few HIP runtime calls the isolated-GEMV timing needs (ctypes; no torch)."""
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+
+    def check(self, rc, what):
+        if rc:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def malloc(self, n):
+        p = self.ct.c_void_p()
+        self.check(self.h.hipMalloc(self.ct.byref(p), self.ct.c_size_t(n)), "hipMalloc")
+        return p
+
+    def h2d(self, dst, arr):
+        a = np.ascontiguousarray(arr)
+        self.check(self.h.hipMemcpy(dst, a.ctypes.data_as(self.ct.c_void_p), self.ct.c_size_t(a.nbytes), 1),
+                   "hipMemcpy")
+
+    def d2d(self, dst, src, n):
+        self.check(self.h.hipMemcpy(dst, src, self.ct.c_size_t(n), 3), "hipMemcpy")
+
+    def event(self):
+        e = self.ct.c_void_p()
+        self.check(self.h.hipEventCreate(self.ct.byref(e)), "hipEventCreate")
+        return e
+
+    def elapsed_ms(self, a, b):
+        self.check(self.h.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = self.ct.c_float()
+        self.check(self.h.hipEventElapsedTime(self.ct.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+    def free(self, p):
+        self.h.hipFree(p)
+
+
+def gemv_report(hip, launches: int = 200, rotate_bytes: int = 640 << 20):
+    """The five isolated Q8_0 GEMV shapes of the 1B model through gg_q8_0_gemv
+    (K -> N: fused QKV, O, gate+up, down, LM head), operands as the workload
+    defines them (q uniform in [-127, 127], |d| lognormal, x ~ N(0, 1)). Each
+    launch reads a different device copy of the weights, cycling over at
+    least rotate_bytes (more than the 256 MB memory-side cache), so the bytes
+    come from HBM; HIP events around `launches` back-to-back launches on one
+    stream give the time per launch, launch gaps included. frac = algorithmic
+    bytes (K N 34/32 + 4 K + 4 N) / time / 8 TB/s."""
+    import ctypes
+    L = capi.lib()
+    out = {}
+    for k, n in ((1152, 1536), (1024, 1152), (1152, 13824), (6912, 1152), (1152, 262144)):
+        blocks, x = synth.gemv_operands(n, k, seed=n + k)
+        psz = capi.lib().gg_q8_0_packed_size(n, k)
+        copies = max(2, -(-rotate_bytes // psz))
+        src = hip.malloc(blocks.nbytes)
+        hip.h2d(src, blocks)
+        w = hip.malloc(psz * copies)
+        if L.gg_q8_0_repack(src, w, n, k, None):
+            raise RuntimeError("gg_q8_0_repack failed")
+        hip.check(hip.h.hipDeviceSynchronize(), "sync")
+        for i in range(1, copies):
+            hip.d2d(ctypes.c_void_p(w.value + i * psz), w, psz)
+        dx, dy = hip.malloc(4 * k), hip.malloc(4 * n)
+        hip.h2d(dx, x)
+        e0, e1 = hip.event(), hip.event()
+        for i in range(min(copies, 16)):   # warm-up
+            L.gg_q8_0_gemv(ctypes.c_void_p(w.value + (i % copies) * psz), dx, dy, n, k, None)
+        hip.check(hip.h.hipEventRecord(e0, None), "hipEventRecord")
+        for i in range(launches):
+            if L.gg_q8_0_gemv(ctypes.c_void_p(w.value + (i % copies) * psz), dx, dy, n, k, None):
+                raise RuntimeError("gg_q8_0_gemv failed")
+        hip.check(hip.h.hipEventRecord(e1, None), "hipEventRecord")
+        us = hip.elapsed_ms(e0, e1) * 1e3 / launches
+        nbytes = k * n // 32 * 34 + 4 * k + 4 * n
+        out[f"{k}x{n}"] = {"us": round(us, 2), "bytes": nbytes, "GBs": round(nbytes / us / 1e3, 1),
+                           "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "floor_us": round(nbytes / (HBM_PEAK_GBS * 1e9) * 1e6, 2), "weight_copies": copies}
+        for p_ in (src, w, dx, dy):
+            hip.free(p_)
+    out["timing"] = (f"HIP events around {launches} back-to-back gg_q8_0_gemv launches on one stream, each on "
+                     f"another device copy of the weights (>= {rotate_bytes >> 20} MiB cycled: HBM, not cache); "
+                     "per-launch time includes the gap between launches")
+    return out
+
+
+def timed_decode(e, shape, tok, pos, steps, warmup, sample=(0.0, 0.9, 1.0), seed=0):
+    """The generate() loop (one step queued ahead, each taking the previous id
+    on the device) for `steps` timed steps after `warmup` synchronous ones;
+    sampling options `sample` with seeded draws. Returns (tok/s, ms per step,
+    mean algorithmic bytes per token, next position)."""
+    rng = np.random.default_rng(seed)
+    draw = (lambda: float(rng.random())) if sample[0] > 0 else (lambda: 0.0)
+    for _ in range(warmup):
+        tok = e.step(tok, pos, *sample, draw())
+        pos += 1
+    p0 = pos
+    e.step_submit(tok, pos, *sample, draw())
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        e.step_submit(-1, pos + 1, *sample, draw())
+        e.step_collect()
+        pos += 1
+    el = time.perf_counter() - t0
+    e.step_collect()
+    nbytes = float(np.mean([step_bytes(shape, q) for q in range(p0, p0 + steps)]))
+    return steps / el, el * 1e3 / steps, nbytes, pos + 1
+
+
+def decode_entry(tok_s, ms, nbytes, extra=None):
+    d = {"tok_s": round(tok_s, 2), "ms_per_step": round(ms, 4), "bytes_per_token": int(nbytes),
+         "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    d.update(extra or {})
+    return d
+
+
+def extra_workloads(shape, tensors, args) -> dict:
+    """The other configurations the reference's benchmark and the workload
+    set name, each driver-timed in this run with its own HBM fraction:
+    sampled decode at 2K (generate()'s defaults T 0.7, top-p 0.9, repetition
+    1.2), reference attention mode at 2K (the JavaScript host's default), the
+    270M model (64-id prompt, 128 greedy steps), the five isolated GEMVs, and
+    sampled decode at 32K KV after three chained turns with KV reuse."""
+    out = {}
+    steps = min(args.steps, 128)
+    prompt = synth.prompt_ids(2048, seed=2048, vocab=shape.vocab)
+    sample = (0.7, 0.9, 1.2)
+
+    # 1B at 2K: sampled (the same weights and attention as the headline run)
+    e = capi.Engine(shape.gg_config(prefill_batch=2048))
+    e.upload_model(tensors)
+    e.finalize()
+    e.penalty_reset()
+    e.penalty_add(prompt)
+    e.prefill(prompt, 0)
+    tok = e.select(*sample, 0.5)
+    r = timed_decode(e, shape, tok, 2048, steps, 8, sample, seed=7)
+    out["decode_1b_2k_sampled"] = decode_entry(*r[:3], {"sampling": "T 0.7, top-p 0.9, repetition 1.2, seeded u",
+                                                         "decode_path": e.decode_path()})
+    e.close()
+    print(f"# sampled 2K: {r[0]:.1f} tok/s", file=sys.stderr, flush=True)
+
+    # 1B at 2K, reference attention mode (full attention, theta 1e6 on every layer)
+    rs = shape.reference_mode()
+    e = capi.Engine(rs.gg_config(prefill_batch=2048))
+    e.upload_model(tensors)
+    e.finalize()
+    e.prefill(prompt, 0)
+    tok = e.select()
+    r = timed_decode(e, rs, tok, 2048, steps, 8)
+    out["decode_1b_2k_reference_mode"] = decode_entry(*r[:3], {"attention": "full on all 26 layers, theta 1e6",
+                                                               "decode_path": e.decode_path()})
+    e.close()
+    print(f"# reference mode 2K: {r[0]:.1f} tok/s", file=sys.stderr, flush=True)
+
+    # 270M: 64-id prompt, TTFT, then 128 greedy steps (contextLength 2048)
+    s270 = synth.GEMMA3_270M.with_ctx(2048).gemma3_mode()
+    t270 = synth.make_model(s270, seed=270)
+    p64 = synth.prompt_ids(64, seed=64, vocab=s270.vocab)
+    e = capi.Engine(s270.gg_config(prefill_batch=64))
+    e.upload_model(t270)
+    e.finalize()
+    ttft = []
+    for _ in range(3):
+        e.reset_kv()
+        t0 = time.perf_counter()
+        e.prefill(p64, 0)
+        tok = e.select()
+        ttft.append(time.perf_counter() - t0)
+    r = timed_decode(e, s270, tok, 64, 128, 0)
+    out["decode_270m"] = decode_entry(*r[:3], {"prompt": 64, "steps": 128, "ttft_ms": round(min(ttft) * 1e3, 3),
+                                               "decode_path": e.decode_path()})
+    e.close()
+    del t270
+    print(f"# 270M: {r[0]:.1f} tok/s, TTFT {min(ttft) * 1e3:.2f} ms", file=sys.stderr, flush=True)
+
+    # isolated GEMVs
+    out["gemv_1b_shapes"] = gemv_report(Hip())
+    print("# GEMV shapes done", file=sys.stderr, flush=True)
+
+    # 32K: three chained turns (16384 + 8192 + 8100 prompt ids, 7 sampled steps
+    # each as generate() writes them), then sampled decode at ~32.7K positions
+    s32 = shape.with_ctx(32768)
+    e = capi.Engine(s32.gg_config(prefill_batch=4096))
+    e.upload_model(tensors)
+    e.finalize()
+    rng = np.random.default_rng(55)
+    kv_pos, tok = 0, 0
+    t0 = time.perf_counter()
+    for turn, n in enumerate((16384, 8192, 8100)):
+        p = synth.prompt_ids(n, seed=300 + turn, vocab=s32.vocab)
+        e.penalty_reset()
+        e.penalty_add(p)
+        e.prefill(p, kv_pos)
+        kv_pos += n
+        tok = e.select(*sample, float(rng.random()))
+        for _ in range(7):
+            tok = e.step(tok, kv_pos, *sample, float(rng.random()))
+            kv_pos += 1
+    fill_s = time.perf_counter() - t0
+    n32 = min(steps, 64)
+    r = timed_decode(e, s32, tok, kv_pos, n32, 0, sample, seed=56)
+    out["decode_1b_32k_sampled"] = decode_entry(*r[:3], {"positions": [kv_pos, kv_pos + n32 - 1],
+                                                         "turns": "16384 + 8192 + 8100 prompt ids, 7 sampled "
+                                                                  "steps each, KV reused across turns",
+                                                         "three_turn_fill_s": round(fill_s, 3),
+                                                         "decode_path": e.decode_path()})
+    e.close()
+    print(f"# 32K sampled: {r[0]:.1f} tok/s", file=sys.stderr, flush=True)
+    return out
+
+
 def copy_calibration(nbytes: int):
     """One device-to-device copy of nbytes (the runtime's copy kernel): the
     reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to
@@ -239,6 +453,8 @@ def main():
                     help="decode path: the persistent kernel (one launch per token) or one kernel per phase")
     ap.add_argument("--sync-steps", action="store_true",
                     help="time synchronous gg_step calls instead of the pipelined loop the JS host runs")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the other workloads (sampled, reference mode, 270M, GEMV shapes, 32K)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the batch-1 token loop runs on "
@@ -375,7 +591,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32; decode FFN activations as 3 int8 planes per 32-block (within 2e-7 of the block max), "
+                 "int32-exact products",
         "data": "synthetic: seeded random-init Q8_0 weights of the Gemma-3-1B architecture, seeded uniform ids",
         "config": {"workload": f"gemma3-1b-q8_0-greedy-decode-after-{args.ctx}", "ctx_prefilled": args.ctx,
                    "batch": 1, "attention": "reference (full, theta 1e6)" if args.reference_mode else
@@ -392,6 +609,8 @@ def main():
                           "device_ms_per_step": round(dev_ms, 4)},
         "prefill": prefill_report(shape, args, prefill_s),
     }
+    if not args.no_extras and args.ctx == 2048 and not args.reference_mode and decode_path == "fused":
+        out["workloads"] = extra_workloads(shape, tensors, args)
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         try:

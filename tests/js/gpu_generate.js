@@ -23,6 +23,7 @@ const backend = Object.assign({}, real, {
     const c = pending.shift();
     if (c.tok < 0) c.tok = lastId;
     c.id = id;
+    c.queued = true;
     lastId = id;
     log.push(c);
     return id;

@@ -362,6 +362,25 @@ async function engineTests() {
     const pfs = gg.calls.filter((c) => c[0] === 'prefill');
     assert.strictEqual(pfs[1][2], 0);  // a fresh conversation from position 0
   });
+  await test('engine: on the graph path (decodePath 0) generate() steps one at a time, never queued', async () => {
+    const seq = new TableGG([215, 216], (p) => (p === 20 ? 106 : 211));
+    const gg = new PipeGG([215, 216], (p) => (p === 20 ? 106 : 211));
+    gg.decodePath = () => 0;   // stepSubmit would run each step synchronously
+    const outs = [];
+    for (const b of [seq, gg]) {
+      const e = await createGemmaEngine({ model: ggufPath, backend: b, contextLength: 64 });
+      e.addUserMessage('Hello');
+      outs.push(await collect(e.generate({ temperature: 0 })));
+    }
+    assert.deepStrictEqual(outs[1], outs[0]);
+    assert.strictEqual(gg.calls.filter((c) => c[0] === 'collect').length, 0);
+    assert.deepStrictEqual(gg.calls.filter((c) => c[0] === 'step'), seq.calls.filter((c) => c[0] === 'step'));
+    gg.decodePath = () => 1;   // the persistent kernel: queued again
+    const e = await createGemmaEngine({ model: ggufPath, backend: gg, contextLength: 64 });
+    e.addUserMessage('Hello');
+    await collect(e.generate({ temperature: 0 }));
+    assert.ok(gg.calls.filter((c) => c[0] === 'collect').length > 0);
+  });
   await test('engine: context overflow resets the KV cache and keeps only the last user message', async () => {
     const { e, gg } = await mk([210, 106, 210, 106]);
     e.addUserMessage('Hello');

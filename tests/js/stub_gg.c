@@ -166,3 +166,6 @@ int gg_step_collect(gg_ctx* c, int32_t* out) {
   *out = g_pending;
   return GG_OK;
 }
+
+/* the stub queues its steps like the persistent decode kernel */
+int gg_decode_path(gg_ctx* c) { return c ? GG_DECODE_FUSED : GG_ERR_INVALID; }

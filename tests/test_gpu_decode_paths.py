@@ -2,7 +2,8 @@
 per token, gg_decode.hip) and the per-kernel graph path compute the same
 functions -- checked against each other at the full 1B shape and against
 the oracle through the model tests -- plus the embedding row read back
-bit-exact and the persistent kernel's timeout report."""
+bit-exact and the persistent kernel's fallback to the graph path when a
+hand-off wait runs out."""
 import os
 
 import numpy as np
@@ -225,25 +226,140 @@ def test_pipelined_steps_match_sequential_steps(gpu, path):
     b.close()
 
 
-def test_persistent_kernel_timeout_is_reported(gpu, tiny_model, monkeypatch):
-    """Every hand-off wait of the persistent kernel is bounded; a wait that
-    runs out raises a host-visible flag and the block leaves, so the launch
-    ends and the call reports a lost device. Forced from the host with a
-    zero spin limit (the first unfinished poll gives up)."""
+def test_persistent_kernel_timeout_falls_back_to_graphs(gpu, monkeypatch):
+    """Every hand-off wait of the persistent kernel is bounded: a launch whose
+    wait runs out raises its flags in mapped host memory and ends. The context
+    then drains its stream, clears the hand-off words and carries on on the
+    graph path, running the timed-out work again there: a token-by-token
+    prefill and synchronous steps (engine a), and pipelined steps -- the one
+    that timed out and the one queued behind it, which took its id on the
+    device (engine b). Both give the graph path's ids and K/V rows. Forced
+    from the host with a zero spin limit (the first poll that finds its words
+    missing gives up); the vocabulary is a multiple of 16384 so that a step
+    is one launch."""
+    shape = synth.Shape(hidden=128, layers=2, n_q=4, inter=256, vocab=16384, ctx=256).gemma3_mode(window=7)
+    t = synth.make_model(shape, seed=7)
+    prompt = synth.prompt_ids(9, seed=11, vocab=shape.vocab)
+    ref_a, ref_b = engine(shape, t, "graph"), engine(shape, t, "graph", prefill_batch=16)
     monkeypatch.setenv("GG_DEC_SPIN_LIMIT", "0")
-    shape = synth.TINY.gemma3_mode(window=7)
-    e = engine(shape, tiny_model, "fused")
+    a, b = engine(shape, t, "fused"), engine(shape, t, "fused", prefill_batch=16)
     monkeypatch.delenv("GG_DEC_SPIN_LIMIT")
-    with pytest.raises(capi.GGError) as ex:
-        for pos in range(4):
-            e.step(5, pos)
-    assert ex.value.code == capi.GG_ERR_DEVICE_LOST
-    assert "persistent decode kernel" in str(ex.value)
-    with pytest.raises(capi.GGError) as ex:
-        e.step(5, 0)
-    assert ex.value.code == capi.GG_ERR_DEVICE_LOST
-    e.close()
-    # a fresh context works
-    e = engine(shape, tiny_model, "fused")
+    assert a.decode_path() == "fused" and b.decode_path() == "fused"
+
+    def run_sync(e):
+        e.prefill(prompt, 0)
+        tok = e.select()
+        ids, pos = [tok], len(prompt)
+        for _ in range(6):
+            tok = e.step(tok, pos)
+            ids.append(tok)
+            pos += 1
+        return ids
+
+    def run_pipelined(e):
+        e.prefill(prompt, 0)   # batched: no persistent launch
+        tok = e.select()
+        ids, pos = [tok], len(prompt)
+        e.step_submit(tok, pos)
+        for k in range(6):
+            if k < 5:
+                e.step_submit(-1, pos + 1)
+            ids.append(e.step_collect())
+            pos += 1
+        return ids
+
+    say("timeout fallback: synchronous")
+    assert run_sync(a) == run_sync(ref_a)
+    assert a.decode_path() == "graph"
+    say("timeout fallback: pipelined")
+    assert run_pipelined(b) == run_pipelined(ref_b)
+    assert b.decode_path() == "graph"
+    n = len(prompt) + 6
+    for e, r in ((a, ref_a), (b, ref_b)):
+        for l in range(shape.layers):
+            for what in (capi.READ_K_CACHE, capi.READ_V_CACHE):
+                got = e.read(what, l).reshape(shape.ctx, 256)[:n]
+                want = r.read(what, l).reshape(shape.ctx, 256)[:n]
+                assert rel(got, want) < 1e-4, (l, what)
+    for e in (a, b, ref_a, ref_b):
+        e.close()
+    # a fresh context runs on the persistent kernel again
+    e = engine(shape, t, "fused")
     e.step(5, 0)
+    assert e.decode_path() == "fused"
+    e.close()
+
+
+def _brev8(c):
+    return int(f"{c:08b}"[::-1], 2)
+
+
+def test_fused_step_ties_follow_the_reference_rule(gpu):
+    """Exact ties on the persistent step's LM head and selection
+    (shaders.ts:327-384). A model's tied embedding copies the row t* that
+    wins a greedy step into rows of t*'s own stride class (lower and higher
+    indices: the same lane in an earlier / later row group of the same wave,
+    another wave's group, a neighbouring lane) and into rows of the classes
+    whose 8-bit bit-reversed ids lie just below and just above t*'s; with an
+    unchanged hidden state their logits equal t*'s bit for bit, the maximum.
+    The fused class candidates and block 0's selection must then give
+    orc.argmax of the read-back logits (the bit-reversed class rule, then the
+    first index; also checked against that rule in closed form),
+    GG_READ_TOPK256 must equal orc.topk256, and sampled steps (T 0.7, top-p
+    0.9, repetition 1.2, three draws) must pick orc.sample_candidates' id."""
+    shape = synth.Shape(hidden=128, layers=2, n_q=4, inter=256, vocab=262144, ctx=256).gemma3_mode(window=7)
+    t = synth.make_model(shape, seed=21)
+    prompt = synth.prompt_ids(9, seed=5, vocab=shape.vocab)
+    pos = len(prompt)
+    e = engine(shape, t, "fused")
+    e.prefill(prompt, 0)
+    tok0 = e.select()
+    e.step(tok0, pos)
+    L = e.read(capi.READ_LOGITS)
+    e.close()
+    ts = int(np.argmax(L))
+    c, k = ts % 256, ts // 256          # class, index inside the class (lane k % 64, row group k // 64)
+    rows = set()
+    for dk in (-256, -64, -1, 1, 64, 256, -512, 512):
+        if 0 <= k + dk < shape.vocab // 256:
+            rows.add(c + 256 * (k + dk))
+    rng = np.random.default_rng(3)
+    for db in (-1, 1):                  # classes whose bit-reversed id is just below / above t*'s
+        b = _brev8(c) + db
+        if 0 <= b < 256:
+            rows.add(_brev8(b) + 256 * int(rng.integers(0, shape.vocab // 256)))
+    rows -= set(int(x) for x in prompt) | {tok0, ts}
+    assert len(rows) >= 6
+    emb = t["token_embd.weight"][2].reshape(shape.vocab, -1).copy()
+    for r in rows:
+        emb[r] = emb[ts]
+    t2 = dict(t)
+    t2["token_embd.weight"] = (t["token_embd.weight"][0], t["token_embd.weight"][1], emb.reshape(-1))
+    e = engine(shape, t2, "fused")
+    assert e.decode_path() == "fused"
+    say("ties", ts, sorted(rows))
+
+    e.prefill(prompt, 0)
+    e.select()
+    g = e.step(tok0, pos)                # greedy
+    L2 = e.read(capi.READ_LOGITS)
+    tied = np.nonzero(L2 == L2.max())[0]
+    assert set(int(i) for i in tied) == rows | {ts}, "the copied rows are the tied maxima"
+    from test_oracle_kernels import closed_form_argmax
+    assert g == orc.argmax(L2) == closed_form_argmax(L2)
+    vals, ids = orc.topk256(L2)
+    top = e.read(capi.READ_TOPK256).view(np.uint32).reshape(256, 2)
+    assert np.array_equal(top[:, 0], vals.view(np.uint32)) and np.array_equal(top[:, 1], ids)
+
+    seen = sorted(set(int(x) for x in prompt) | {tok0})
+    for u in (0.02, 0.5, 0.97):
+        e.prefill(prompt, 0)
+        e.select()
+        e.penalty_reset()
+        e.penalty_add(np.array(seen, np.int32))
+        s = e.step(tok0, pos, 0.7, 0.9, 1.2, u)
+        L3 = e.read(capi.READ_LOGITS)
+        assert np.array_equal(L3.view(np.uint32), L2.view(np.uint32))
+        v3, i3 = orc.topk256(L3)
+        assert s == orc.sample_candidates(v3, i3, seen, 0.7, 0.9, 1.2, u), u
     e.close()

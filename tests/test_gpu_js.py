@@ -1,8 +1,9 @@
 """The JavaScript host on the GPU through the Node-API binding: two generate()
 turns (greedy, then sampled with a seeded draw) on a tiny GGUF written by
-gemma_amd.gguf. generate() keeps one step queued ahead (stepSubmit /
-stepCollect, each step taking the previous id on the device); every
-collected step is logged with its input id resolved. The binding calls the
+gemma_amd.gguf. On the persistent kernel's path generate() keeps one step
+queued ahead (stepSubmit / stepCollect, each step taking the previous id on
+the device); every collected step is logged with its input id resolved. On
+the graph path (GG_DECODE=graph) it awaits each step. The binding calls the
 host made are replayed through the Python C-ABI binding as sequential steps
 and must give the same ids (a step queued past a turn's end included); the
 greedy turn must also match the oracle."""
@@ -25,18 +26,25 @@ NODE = shutil.which("node")
 
 
 @pytest.mark.skipif(NODE is None, reason="node is not installed")
-@pytest.mark.parametrize("attention", ["reference", "gemma3"])
-def test_js_host_on_gpu(gpu, tmp_path, attention):
-    say("js host", attention)
+@pytest.mark.parametrize("attention,path", [("reference", "fused"), ("gemma3", "fused"), ("gemma3", "graph")])
+def test_js_host_on_gpu(gpu, tmp_path, attention, path):
+    say("js host", attention, path)
     shape = synth.TINY.with_ctx(256)
     tensors = synth.make_model(shape, seed=9)
     g = str(tmp_path / "tiny.gguf")
     synth.write_model_gguf(g, shape, tensors=tensors)
+    env = dict(os.environ)
+    if path == "graph":
+        env["GG_DECODE"] = "graph"   # the binding then reports decodePath 0
     r = subprocess.run([NODE, os.path.join(HERE, "js", "gpu_generate.js"), g, attention], stdout=subprocess.PIPE,
-                       stderr=subprocess.PIPE, text=True, timeout=120)
+                       stderr=subprocess.PIPE, text=True, timeout=120, env=env)
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
     log = out["log"]
+    # generate() queues steps only on the persistent kernel's path; on the
+    # graph path a queued submit would block the event loop
+    queued = [c for c in log if c.get("queued")]
+    assert (len(queued) > 0) == (path == "fused"), path
     run_shape = shape.gemma3_mode(window=512) if attention == "gemma3" else shape.reference_mode()
 
     # replay the same calls through the Python binding of the C-ABI

@@ -137,6 +137,56 @@ def test_1b_batched_prefill_ragged_slices_long_span(gpu):
     b.close()
 
 
+def test_1b_batched_prefill_32k_matches_token_path_and_oracle(gpu):
+    """Gemma-3-1B at contextLength 32768, gemma3 attention: a 32760-id prompt
+    prefilled in batched slices of 4096 rows (the global layers' prefill
+    attention over key spans up to 32760) against the token-by-token path on
+    the persistent kernel: every layer's hidden state, the normed hidden and
+    the K/V rows of the global layers 5, 11, 17 and 23 over all 32760
+    positions. Then the oracle takes the batched engine's K/V cache and both
+    run 8 greedy steps from position 32760: per-layer hidden, logits and ids
+    against the oracle at every step."""
+    shape = synth.GEMMA3_1B.with_ctx(32768).gemma3_mode()
+    n = 32760
+    say("1b 32k batched prefill vs token path")
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    prompt = synth.prompt_ids(n, seed=32760, vocab=shape.vocab)
+    a = engine(shape, t, 4096)
+    a.prefill(prompt, 0)
+    b = engine(shape, t, 0)
+    b.prefill(prompt, 0)
+    say("1b 32k prefilled both")
+    for l in range(shape.layers):
+        assert rel(a.read(capi.READ_LAYER_HIDDEN, l), b.read(capi.READ_LAYER_HIDDEN, l)) < TOL, l
+    assert rel(a.read(capi.READ_NORMED), b.read(capi.READ_NORMED)) < TOL
+    for l in (5, 11, 17, 23):
+        for what in (capi.READ_K_CACHE, capi.READ_V_CACHE):
+            ka = a.read(what, l).reshape(shape.ctx, 256)[:n]
+            kb = b.read(what, l).reshape(shape.ctx, 256)[:n]
+            assert rel(ka, kb) < TOL, (l, what)
+    b.close()
+    o = orc.OracleModel(shape, t)
+    for l in range(shape.layers):
+        o.buffer(orc.GOR_K_CACHE, l)[:] = a.read(capi.READ_K_CACHE, l)
+        o.buffer(orc.GOR_V_CACHE, l)[:] = a.read(capi.READ_V_CACHE, l)
+    tok, pos = int(prompt[-1]), n - 1
+    # the prompt's last row again as a decode step (the same K/V row), then 8 steps
+    for step in range(9):
+        nxt = a.step(tok, pos)
+        o.forward(tok, pos)
+        ref = o.select()
+        for l in range(shape.layers):
+            assert rel(a.read(capi.READ_LAYER_HIDDEN, l), o.buffer(orc.GOR_LAYER_HIDDEN, l)) < TOL, (step, l)
+        assert rel(a.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL, step
+        assert nxt == ref, f"step {step}"
+        say("1b 32k step", step, nxt)
+        tok, pos = nxt, pos + 1
+    o.close()
+    a.close()
+
+
 def test_270m_batched_prefill_matches_oracle(gpu):
     """Gemma-3-270M architecture (hidden 640: 128-wide GEMM tiles with a K
     split, 64-row prompt), gemma3 attention: the 64-id prompt in one batched

@@ -238,9 +238,19 @@ __device__ __forceinline__ void stamp(const DecodeArgs& a, int b, int l, int ev)
     a.timeline[((size_t)b * a.L + l) * kDecEvents + ev] = __builtin_amdgcn_s_memrealtime();
 }
 
-__device__ __forceinline__ void report_timeout(const DecodeArgs& a) {
-  if (tidx() == 0)
+// A block whose hand-off wait ran out (called by every thread of the block):
+// raises the launch's flags in mapped host memory and, when fewer than all
+// blocks of this launch have started (their arrival words lack this epoch),
+// records how many had: the launch was not co-resident.
+__device__ __forceinline__ void report_timeout(const DecodeArgs& a, uint32_t epoch) {
+  const int tid = tidx();
+  const bool here = __hip_atomic_load(a.arrive + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch + 1;
+  const int n = __syncthreads_count(here);
+  if (tid == 0) {
+    if (n < kDecBlocks) __hip_atomic_store(a.host_out + 2, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.host_out + 8 + a.out_slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(a.host_out + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // Block-uniform failure check after a poll (one barrier).
@@ -1073,6 +1083,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   const int cur = args_in ? -1 : st->cursor;
   const int token = args_in ? (a.in_token >= 0 ? a.in_token : st->out_token) : cur < 0 ? st->token : a.tokens[cur];
   const uint32_t base = epoch * (uint32_t)(a.L + 2);
+  if (tid == 0) __hip_atomic_store(a.arrive + b, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
 
   const int Kq = H / 64;
@@ -1141,7 +1152,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     auto update_resid = [&]() __attribute__((always_inline)) {
       float dv[kEPT], wpost[kEPT];
       load_norm(norm_of(a, layer_view(a, l - 1), 5), H, wpost);
-      const bool ok = ll_wait<kEPT>(a.x_down, H, tag - 1, dv, lim);
+      const bool ok = ll_wait<kEPT>(a.x_down + ((l - 1) & 1) * kDecXW, H, tag - 1, dv, lim);
       soft_fail(S, ok);
       stamp(a, b, l, 1);
       if (qb) {
@@ -1171,19 +1182,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       stamp(a, b, l, 2);
       if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
         // long span: every block takes a chunk of the four heads
-        if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
+        if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a, epoch); return; }
         stamp(a, b, l, 14);
       } else if (Ly.window == 0 && b < 64) {
         // full-attention layers: blocks [0, 64) also take chunks 16..31
         const int c = 16 + (b & 7) + 8 * (b >> 5), h = (b >> 3) & 3;
-        if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a); return; }
+        if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a, epoch); return; }
       }
       issue_ffn();
     } else if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
       // ---- A, long span: chunk b of the four heads, then the merge ----
-      if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
+      if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a, epoch); return; }
       stamp(a, b, l, 2);
-      if (!merge_long(a, S, l, b - kDecQBlocks, tag)) { report_timeout(a); return; }
+      if (!merge_long(a, S, l, b - kDecQBlocks, tag)) { report_timeout(a, epoch); return; }
       stamp(a, b, l, 3);
       issue_ffn();
     } else {
@@ -1192,14 +1203,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       const int c = (ab & 7) + 8 * (ab >> 5), h = (ab >> 3) & 3;
       const bool glob = Ly.window == 0;
       if (!attention_block(a, S, Ly, l, c, h, pos, tag, glob ? kDecChunksG : kDecChunks)) {
-        report_timeout(a);
+        report_timeout(a, epoch);
         return;
       }
       stamp(a, b, l, 2);
       if (c < 4) {
         const bool mok =
             glob ? merge_head_part<kDecChunksG>(a, S, l, h, c, tag) : merge_head_part<kDecChunks>(a, S, l, h, c, tag);
-        if (!mok) { report_timeout(a); return; }
+        if (!mok) { report_timeout(a, epoch); return; }
         stamp(a, b, l, 3);
       }
       if (l > 0 && defer) update_resid();
@@ -1213,7 +1224,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       mg_issue<8, 1>(Ly.o, a.QD / 64, a.kps_o, b * a.kps_o, a.kps_o, wo);
       zero_red(S.red);
       const bool ok = poll_to_xs<kAttnMaxQ * kHeadDim / NT>(S, a.x_attn, a.QD, tag, lim);
-      if (failed(S, ok)) { report_timeout(a); return; }
+      if (failed(S, ok)) { report_timeout(a, epoch); return; }
       stamp(a, b, l, 3);
       mg_dots<8, 1>(wo, (const float*)S.xs4, a.QD / 64, a.kps_o, b, b * a.kps_o, a.kps_o, S.red);
       __syncthreads();
@@ -1323,12 +1334,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
         float sum = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) sum += S.red[w][tid];
-        ll_st(a.x_down + 8 * b + tid, sum, tag);
+        ll_st(a.x_down + (l & 1) * kDecXW + 8 * b + tid, sum, tag);
       }
       stamp(a, b, l, 11);
     }
     __syncthreads();
-    if (S.fail) { report_timeout(a); return; }
+    if (S.fail) { report_timeout(a, epoch); return; }
   }
 
   // ---- end of the pass: post-FFN norm + residual, output norm ----
@@ -1359,11 +1370,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     float dv[kEPT], wpost[kEPT], wout[kEPT];
     load_norm(norm_of(a, layer_view(a, a.L - 1), 5), H, wpost);
     load_norm(a.out_norm, H, wout);
-    const bool ok = ll_wait<kEPT>(a.x_down, H, tagL, dv, lim);
+    const bool ok = ll_wait<kEPT>(a.x_down + ((a.L - 1) & 1) * kDecXW, H, tagL, dv, lim);
     soft_fail(S, ok);
     resid_norm<true>(S, dv, wpost, wout, H, a.eps, r);
     __syncthreads();
-    if (S.fail) { report_timeout(a); return; }
+    if (S.fail) { report_timeout(a, epoch); return; }
     if (b == 0) {
       const float* xs = (const float*)S.xs4;
 #pragma unroll
@@ -1480,7 +1491,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       if (now_ - t0 > lim) { ok = false; break; }
     }
   }
-  if (failed(S, ok)) { report_timeout(a); return; }
+  if (failed(S, ok)) { report_timeout(a, epoch); return; }
   if (tid < 256) {
     a.top[2 * tid] = __float_as_uint(m);
     a.top[2 * tid + 1] = id;
@@ -1514,7 +1525,7 @@ int decode_occupancy() {
   return occ;
 }
 
-int launch_decode(int mode, const DecodeArgs& a, void* stream) {
+int launch_decode(int mode, const DecodeArgs& a, void* stream, bool coop) {
   hipStream_t s = (hipStream_t)stream;
   if (mode == DEC_STEP && !a.lm) return (int)hipErrorInvalidValue;
   if (a.H > kDecMaxH || a.g_f > kDecMaxFBlocks) return (int)hipErrorInvalidValue;
@@ -1522,17 +1533,19 @@ int launch_decode(int mode, const DecodeArgs& a, void* stream) {
   // a step whose sampling options are arguments and greedy takes the copy
   // without the sampler
   const bool sample = !(a.in_use && a.in_temperature == 0.0 && a.in_rep_penalty <= 1.0);
+  const void* k;
   if (mode == DEC_FWD) {
-    if (a.long_ctx) hipLaunchKernelGGL((k_decode<DEC_FWD, true, false>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_decode<DEC_FWD, false, false>), grid, block, 0, s, a);
+    k = a.long_ctx ? (const void*)k_decode<DEC_FWD, true, false> : (const void*)k_decode<DEC_FWD, false, false>;
   } else if (a.long_ctx) {
-    if (sample) hipLaunchKernelGGL((k_decode<DEC_STEP, true, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_decode<DEC_STEP, true, false>), grid, block, 0, s, a);
+    k = sample ? (const void*)k_decode<DEC_STEP, true, true> : (const void*)k_decode<DEC_STEP, true, false>;
   } else {
-    if (sample) hipLaunchKernelGGL((k_decode<DEC_STEP, false, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_decode<DEC_STEP, false, false>), grid, block, 0, s, a);
+    k = sample ? (const void*)k_decode<DEC_STEP, false, true> : (const void*)k_decode<DEC_STEP, false, false>;
   }
-  return (int)hipGetLastError();
+  DecodeArgs arg = a;
+  void* args[] = {&arg};
+  if (coop) return (int)hipLaunchCooperativeKernel(k, grid, block, args, 0, s);
+  const hipError_t e = hipLaunchKernel(k, grid, block, args, 0, s);
+  return e != hipSuccess ? (int)e : (int)hipGetLastError();
 }
 
 }  // namespace gg

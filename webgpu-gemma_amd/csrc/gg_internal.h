@@ -234,6 +234,7 @@ constexpr int kDecPart = kHeadDim + 2;   // LL words of one chunk partial: o[256
 constexpr int kDecMaxRows = 128;     // rows of one phase a block may own
 constexpr int kDecMaxH = 1280;       // hidden sizes of the persistent kernel (its W_down rows per thread)
 constexpr int kDecMaxFBlocks = 256;  // FFN blocks: intermediate / 32 <= 256
+constexpr int kDecXW = 2048;        // LL words of one all-gathered hidden-size row (H <= kDecMaxH)
 constexpr int kDecMaxCtx = 4096;     // spans up to 4096: 16 / 32 chunks per head, one head per block
 constexpr int kDecChunksL = 256;     // longer spans of full-attention layers: chunk b of all four heads in block b
 enum DecMode { DEC_FWD = 0, DEC_STEP = 1 };
@@ -273,8 +274,10 @@ struct DecodeArgs {
   uint64_t* x_attn;        // [QD]
   uint64_t* x_o;           // [H]
   uint64_t* x_dpart;       // [g_f][H] partial down outputs
-  uint64_t* x_down;        // [H]
+  uint64_t* x_down;        // [2][kDecXW]: layer l's down output in row l & 1, so a block that
+                           // polls layer l - 1's row late never finds it overwritten by layer l's
   uint64_t* x_cand;        // [256][2]: per vocab class (value, id)
+  uint32_t* arrive;        // [kDecBlocks]: block b stores epoch + 1 at its start (residency check on a timeout)
   // parity outputs
   float* hidden;
   float* normed;
@@ -284,7 +287,9 @@ struct DecodeArgs {
   float* logits;           // DEC_STEP: [V] class-major
   uint32_t* top;           // [256] x {f32 bits, id}
   uint32_t* seen;          // penalty bitmap
-  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag, [4..5] pipelined tokens
+  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag, [2] blocks a timed-out
+                           // block found started when fewer than all (0: all), [4..5] pipelined tokens,
+                           // [8 + out_slot] timeout flag of the launch that writes host_out[out_slot]
   long long spin_limit;    // s_memrealtime ticks (100 MHz) one hand-off may wait
   long long* timeline;     // optional [256][L][kDecEvents] s_memrealtime stamps (null: off)
   // in_use != 0: this launch's position, token and sampling parameters are
@@ -299,7 +304,9 @@ struct DecodeArgs {
   int32_t long_ctx;
 };
 constexpr int kDecEvents = 16;  // timeline events per (block, layer)
-int launch_decode(int mode, const DecodeArgs& a, void* stream);
+// coop: a cooperative launch (hipLaunchCooperativeKernel), for launches
+// outside stream capture.
+int launch_decode(int mode, const DecodeArgs& a, void* stream, bool coop);
 // Blocks of the persistent kernel one CU can hold (it needs 1).
 int decode_occupancy();
 

@@ -144,8 +144,14 @@ struct gg_ctx {
   bool pipe_launched[2] = {false, false};   // slot's step is a launch in flight (else its id is known)
   int32_t pipe_tok[2] = {0, 0};       // ids of steps that ran synchronously
   hipEvent_t pipe_ev[2] = {nullptr, nullptr};
+  struct PipeArgs { int32_t token, pos; gg_sample s; double u; };
+  PipeArgs pipe_args[2] = {};         // each outstanding step's arguments (re-run after a fallback)
   bool have_prev = false;             // a selection has run: a step may take its id on the device
   int32_t last_tok = 0;               // ... that id, when the host knows it
+  int32_t sel_id = 0;                 // id of the last selection whose result the host has
+  hipEvent_t fence_ev = nullptr;      // follows this context's latest persistent launch (shared device)
+  bool fence_reg = false;             // registered as a persistent-kernel context of its device
+  bool coop = false;                  // GG_DEC_COOP=1: direct persistent launches are cooperative
   bool logits_cm = false;             // the last logits are in class-major order
   long long* timeline = nullptr;      // GG_DEC_TIMELINE=1: phase stamps of the last launch
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -253,9 +259,57 @@ std::string fused_unsupported(gg_ctx* c) {
   return "";
 }
 
-// Start a persistent-kernel launch: clear the hand-off words (and the
-// launch counter that feeds their tags) before the 32-bit tags could wrap.
-int fused_launch_begin(gg_ctx* c) {
+// Persistent launches of every context of the process on one device run one
+// at a time: a launch needs all 256 of its blocks resident, and two launches
+// side by side would each hold part of the CUs until their hand-off waits ran
+// out. While a device has more than one persistent-kernel context, every
+// persistent launch records its context's fence event, and a launch from
+// another context first waits for the latest one.
+int sync(gg_ctx* c, const char* what);
+constexpr int kMaxFenceDevices = 64;
+struct DevFence {
+  std::vector<gg_ctx*> ctxs;   // persistent-kernel contexts of the device
+  gg_ctx* last = nullptr;      // whose fence event follows the device's latest persistent launch
+};
+std::mutex g_fence_mu;
+DevFence g_fence[kMaxFenceDevices];
+
+int fence_register(gg_ctx* c) {
+  if (c->device < 0 || c->device >= kMaxFenceDevices) return set_err(c, GG_ERR_INVALID, "device index");
+  std::lock_guard<std::mutex> lk(g_fence_mu);
+  DevFence& f = g_fence[c->device];
+  if (f.ctxs.size() == 1) {
+    // the device's only context has not fenced its launches so far
+    gg_ctx* o = f.ctxs[0];
+    GG_HIP(c, hipEventRecord(o->fence_ev, o->stream));
+    f.last = o;
+  }
+  f.ctxs.push_back(c);
+  c->fence_reg = true;
+  return GG_OK;
+}
+
+void fence_unregister(gg_ctx* c) {
+  if (!c->fence_reg) return;
+  std::lock_guard<std::mutex> lk(g_fence_mu);
+  DevFence& f = g_fence[c->device];
+  for (size_t i = 0; i < f.ctxs.size(); ++i)
+    if (f.ctxs[i] == c) {
+      f.ctxs.erase(f.ctxs.begin() + (long)i);
+      break;
+    }
+  if (f.last == c) f.last = nullptr;
+  c->fence_reg = false;
+}
+
+// Start a persistent-kernel launch (lk holds the device's launch order until
+// persistent_end): wait for another context's latest launch, and clear the
+// hand-off words (and the launch counter that feeds their tags) before the
+// 32-bit tags could wrap.
+int persistent_begin(gg_ctx* c, std::unique_lock<std::mutex>& lk) {
+  lk = std::unique_lock<std::mutex>(g_fence_mu);
+  DevFence& f = g_fence[c->device];
+  if (f.last && f.last != c) GG_HIP(c, hipStreamWaitEvent(c->stream, f.last->fence_ev, 0));
   const uint64_t limit = 0xffffffffull / (uint64_t)(c->L + 2) - 2;
   if (c->dec_launches >= limit) {
     GG_HIP(c, hipMemsetAsync(c->xll, 0, c->xll_words * 8, c->stream));
@@ -266,14 +320,41 @@ int fused_launch_begin(gg_ctx* c) {
   return GG_OK;
 }
 
-int check_fused(gg_ctx* c) {
-  if (c->fused && c->h_out[1] != 0) {
-    c->lost = true;
-    return set_err(c, GG_ERR_DEVICE_LOST,
-                   "device lost: a hand-off of the persistent decode kernel timed out (its 256 blocks were not all "
-                   "resident)");
+int persistent_end(gg_ctx* c) {
+  DevFence& f = g_fence[c->device];
+  if (f.ctxs.size() > 1) {
+    GG_HIP(c, hipEventRecord(c->fence_ev, c->stream));
+    f.last = c;
   }
   return GG_OK;
+}
+
+// Every hand-off wait of the persistent kernel is bounded, so a launch whose
+// blocks were not all resident (CUs held by another process's work) or that
+// stalled ends with its flags raised in mapped host memory. The context then
+// drains its stream, clears the hand-off words and continues on the graph
+// path (one kernel per phase, nothing to keep resident); the caller re-runs
+// the work. Returns kRetry after that switch, GG_OK when no flag is raised.
+constexpr int kRetry = 1;
+int fall_back_to_graphs(gg_ctx* c) {
+  GG_TRY(sync(c, "persistent decode kernel"));
+  const int resident = c->h_out[2];
+  for (int i : {1, 2, 8, 12, 13}) c->h_out[i] = 0;
+  GG_HIP(c, hipMemsetAsync(c->xll, 0, c->xll_words * 8, c->stream));
+  GG_HIP(c, hipMemsetAsync((char*)c->st + offsetof(DevState, epoch), 0, 4, c->stream));
+  GG_TRY(sync(c, "hand-off reset"));
+  c->dec_launches = 0;
+  c->fused = c->fused_step = false;
+  fence_unregister(c);
+  c->fused_why = resident > 0 ? "a persistent decode launch found only " + std::to_string(resident) +
+                                    " of its 256 blocks started (the GPU is shared); switched to the graph path"
+                              : "a hand-off of the persistent decode kernel timed out; switched to the graph path";
+  return kRetry;
+}
+
+int check_fused(gg_ctx* c) {
+  if (!c->fused || c->h_out[1] == 0) return GG_OK;
+  return fall_back_to_graphs(c);
 }
 
 GemvArgs gemv_base(const uint8_t* W, const Q8Layout& L, float* out) {
@@ -395,7 +476,7 @@ int record_forward_impl(gg_ctx* c, bool final_norm) {
 int record_forward(gg_ctx* c) { return record_forward_impl(c, true); }
 
 int record_fused_fwd(gg_ctx* c) {
-  return launch_rc(c, launch_decode(DEC_FWD, c->dargs, c->stream), "persistent decode kernel");
+  return launch_rc(c, launch_decode(DEC_FWD, c->dargs, c->stream, false), "persistent decode kernel");
 }
 
 // Record LM head + selection (engine.ts:805-902). With `fused_final` the LM
@@ -485,15 +566,16 @@ int launch_fused_step(gg_ctx* c) {
   a.in_top_p = c->h_st->top_p;
   a.in_rep_penalty = c->h_st->rep_penalty;
   a.in_u = c->h_st->u;
-  return launch_rc(c, launch_decode(DEC_STEP, a, c->stream), "persistent decode kernel");
+  return launch_rc(c, launch_decode(DEC_STEP, a, c->stream, c->coop), "persistent decode kernel");
 }
 
 int run_forward(gg_ctx* c) {
   if (c->fused) {
-    GG_TRY(fused_launch_begin(c));
+    std::unique_lock<std::mutex> lk;
+    GG_TRY(persistent_begin(c, lk));
     if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_ffwd, c->stream));
     else GG_TRY(record_fused_fwd(c));
-    return GG_OK;
+    return persistent_end(c);
   }
   if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fwd, c->stream));
   else GG_TRY(record_forward(c));
@@ -992,18 +1074,19 @@ int gg_finalize(gg_ctx* c) {
     DecodeArgs& d = c->dargs;
     // hand-off words; polled buffers hold kDecThreads * (words per thread)
     const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunksL * kDecPart;
-    const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = 2048, w_dpart = (size_t)(c->I / 32) * c->H;
-    const size_t w_cand = 512;
-    c->xll_words = w_qkv + w_part + w_attn + 2 * w_h + w_dpart + w_cand;
+    const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = kDecXW, w_dpart = (size_t)(c->I / 32) * c->H;
+    const size_t w_cand = 512, w_arrive = kDecBlocks / 2;
+    c->xll_words = w_qkv + w_part + w_attn + 3 * w_h + w_dpart + w_cand + w_arrive;
     GG_TRY(dalloc(c, &c->xll, c->xll_words * 8));
     GG_HIP(c, hipMemset(c->xll, 0, c->xll_words * 8));
     d.x_qkv = c->xll;
     d.x_part = d.x_qkv + w_qkv;
     d.x_attn = d.x_part + w_part;
     d.x_o = d.x_attn + w_attn;
-    d.x_down = d.x_o + w_h;
-    d.x_dpart = d.x_down + w_h;
+    d.x_down = d.x_o + w_h;   // two rows, by layer parity
+    d.x_dpart = d.x_down + 2 * w_h;
     d.x_cand = d.x_dpart + w_dpart;
+    d.arrive = (uint32_t*)(d.x_cand + w_cand);
     d.w_qkv = c->s_qkv;
     d.w_o = c->s_o;
     d.w_guf = c->s_guf;
@@ -1061,6 +1144,12 @@ int gg_finalize(gg_ctx* c) {
     // GG_DEC_SPIN_LIMIT=<ticks>: a shorter bound (tests force the timeout path)
     const char* sl = getenv("GG_DEC_SPIN_LIMIT");
     if (sl && sl[0]) d.spin_limit = atoll(sl);
+    // GG_DEC_COOP=1: the persistent kernel's direct launches are cooperative
+    // launches (the runtime then refuses a grid that cannot be resident)
+    const char* co = getenv("GG_DEC_COOP");
+    c->coop = co && co[0] == '1';
+    GG_HIP(c, hipEventCreateWithFlags(&c->fence_ev, hipEventDisableTiming | hipEventDisableSystemFence));
+    GG_TRY(fence_register(c));
     // GG_DEC_TIMELINE=1: the persistent kernel stamps its phases (profiling)
     const char* tl = getenv("GG_DEC_TIMELINE");
     if (tl && tl[0] == '1') {
@@ -1106,10 +1195,17 @@ int gg_prefill(gg_ctx* c, const int32_t* tokens, int32_t n, int32_t start_pos) {
     c->timed = c->probed = false;
     return sync(c, "prefill");
   }
-  for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
-  c->timed = c->probed = false;
-  GG_TRY(sync(c, "prefill"));
-  return check_fused(c);
+  for (;;) {
+    for (int i = 0; i < n; ++i) GG_TRY(run_forward(c));
+    c->timed = c->probed = false;
+    GG_TRY(sync(c, "prefill"));
+    const int r = check_fused(c);
+    if (r != kRetry) return r;
+    // after a fallback the graph path runs the prompt again from its first token
+    c->h_st->pos = start_pos;
+    c->h_st->cursor = 0;
+    GG_TRY(push_state(c, 0, offsetof(DevState, temperature)));
+  }
 }
 
 static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bool with_forward) {
@@ -1118,18 +1214,28 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   c->h_st->rep_penalty = s->rep_penalty;
   c->h_st->u = u;
   const bool ev = c->step_timing;   // three event records cost ~9 us of device time per step
+  // a persistent launch whose hand-offs timed out leaves the context on the
+  // graph path (check_fused), and the selection runs again there
+#define GG_CHECK_FUSED_RETRY()                                          \
+  do {                                                                  \
+    const int r_ = check_fused(c);                                      \
+    if (r_ == kRetry) return select_impl(c, s, u, out, with_forward);   \
+    if (r_ != GG_OK) return r_;                                         \
+  } while (0)
   if (with_forward && !ev) {
     if (c->fused) {
-      GG_TRY(fused_launch_begin(c));
+      std::unique_lock<std::mutex> lk;
+      GG_TRY(persistent_begin(c, lk));
       if (c->fused_step) GG_TRY(launch_fused_step(c));
       else if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_fstep, c->stream));
       else GG_TRY(record_fused_step(c));
+      GG_TRY(persistent_end(c));
     } else {
       if (c->use_graphs) GG_HIP(c, hipGraphLaunch(c->g_step, c->stream));
       else GG_TRY(record_step(c));
     }
     GG_TRY(sync(c, "step"));
-    GG_TRY(check_fused(c));
+    GG_CHECK_FUSED_RETRY();
     c->logits_cm = c->fused_step;
     c->timed = false;
     c->probed = true;
@@ -1139,13 +1245,17 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (with_forward && c->fused && c->fused_step) {
     // timed persistent step: the whole token is one launch (forward, LM
     // head and selection), reported as the forward time with select 0
-    GG_TRY(fused_launch_begin(c));
-    GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
-    GG_TRY(launch_fused_step(c));
-    GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
-    GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
+    {
+      std::unique_lock<std::mutex> lk;
+      GG_TRY(persistent_begin(c, lk));
+      GG_HIP(c, hipEventRecord(c->ev[0], c->stream));
+      GG_TRY(launch_fused_step(c));
+      GG_HIP(c, hipEventRecord(c->ev[1], c->stream));
+      GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
+      GG_TRY(persistent_end(c));
+    }
     GG_TRY(sync(c, "step"));
-    GG_TRY(check_fused(c));
+    GG_CHECK_FUSED_RETRY();
     c->logits_cm = true;
     c->timed = true;
     c->probed = true;
@@ -1165,7 +1275,8 @@ static int select_impl(gg_ctx* c, const gg_sample* s, double u, int32_t* out, bo
   if (ev) GG_HIP(c, hipEventRecord(c->ev[2], c->stream));
   // the selector stores the token straight into the mapped host word
   GG_TRY(sync(c, with_forward ? "step" : "select"));
-  GG_TRY(check_fused(c));
+  GG_CHECK_FUSED_RETRY();
+#undef GG_CHECK_FUSED_RETRY
   c->logits_cm = false;
   c->timed = ev;
   c->probed = true;
@@ -1179,6 +1290,7 @@ int gg_select(gg_ctx* c, const gg_sample* s, double u, int32_t* out_token) {
   GG_TRY(select_impl(c, s, u, out_token, false));
   c->have_prev = true;
   c->last_tok = *out_token;
+  c->sel_id = *out_token;
   return GG_OK;
 }
 
@@ -1192,6 +1304,7 @@ static int step_impl(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, 
   GG_TRY(select_impl(c, s, u, out_token, true));
   c->have_prev = true;
   c->last_tok = *out_token;
+  c->sel_id = *out_token;
   return GG_OK;
 }
 
@@ -1211,7 +1324,8 @@ int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, do
   if (c->fused && c->fused_step) {
     // one launch, queued behind the previous one; with token < 0 it embeds
     // the id that launch selects (DevState::out_token, read on the device)
-    GG_TRY(fused_launch_begin(c));
+    std::unique_lock<std::mutex> lk;
+    GG_TRY(persistent_begin(c, lk));
     DecodeArgs a = c->dargs;
     a.in_use = 1;
     a.in_pos = pos;
@@ -1221,8 +1335,10 @@ int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, do
     a.in_rep_penalty = s->rep_penalty;
     a.in_u = u;
     a.out_slot = 4 + slot;
-    GG_TRY(launch_rc(c, launch_decode(DEC_STEP, a, c->stream), "persistent decode kernel"));
+    GG_TRY(launch_rc(c, launch_decode(DEC_STEP, a, c->stream, c->coop), "persistent decode kernel"));
     GG_HIP(c, hipEventRecord(c->pipe_ev[slot], c->stream));
+    GG_TRY(persistent_end(c));
+    c->pipe_args[slot] = {token, pos, *s, u};
     c->pipe_launched[slot] = true;
     c->logits_cm = true;
     c->timed = false;
@@ -1248,12 +1364,29 @@ int gg_step_collect(gg_ctx* c, int32_t* out_token) {
   c->pipe_n -= 1;
   if (c->pipe_launched[slot]) {
     GG_HIP(c, hipEventSynchronize(c->pipe_ev[slot]));
-    GG_TRY(check_fused(c));
+    if (c->h_out[12 + slot] != 0) {
+      // this step's launch timed out, and a step queued behind it took its
+      // id on the device: switch to the graph path and run both again there
+      // with the ids the host now has
+      const int nxt = slot ^ 1;
+      const bool redo_next = c->pipe_n > 0 && c->pipe_launched[nxt];
+      const int r = fall_back_to_graphs(c);
+      if (r != kRetry) return r;
+      const gg_ctx::PipeArgs pa = c->pipe_args[slot], pb = c->pipe_args[nxt];
+      GG_TRY(step_impl(c, pa.token >= 0 ? pa.token : c->sel_id, pa.pos, &pa.s, pa.u, out_token));
+      if (redo_next) {
+        GG_TRY(step_impl(c, pb.token >= 0 ? pb.token : *out_token, pb.pos, &pb.s, pb.u, &c->pipe_tok[nxt]));
+        c->pipe_launched[nxt] = false;
+      }
+      c->sel_id = *out_token;
+      return GG_OK;
+    }
     *out_token = c->h_out[4 + slot];
     if (c->pipe_n == 0) c->last_tok = *out_token;
   } else {
     *out_token = c->pipe_tok[slot];
   }
+  c->sel_id = *out_token;
   return GG_OK;
 }
 
@@ -1403,6 +1536,8 @@ const char* gg_last_error(const gg_ctx* c) { return c ? c->err.c_str() : g_creat
 void gg_destroy(gg_ctx* c) {
   if (!c) return;
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  fence_unregister(c);
+  if (c->fence_ev) (void)hipEventDestroy(c->fence_ev);
   if (c->g_fwd) (void)hipGraphExecDestroy(c->g_fwd);
   if (c->g_sel) (void)hipGraphExecDestroy(c->g_sel);
   if (c->g_step) (void)hipGraphExecDestroy(c->g_step);

@@ -210,7 +210,12 @@ class GemmaEngineImpl {
     const isStop = (t) => t === 1 || t === 0 || t === 106;
     yield this.tokenizer.decodeToken(next);
 
-    if (typeof this.gg.stepSubmit === 'function' && typeof this.gg.stepCollect === 'function') {
+    // the queued loop only where a submit returns before its step has run
+    // (the persistent decode kernel: decodePath 1); on the graph path the
+    // binding's stepSubmit would run each step synchronously on this thread
+    const queued = typeof this.gg.stepSubmit === 'function' && typeof this.gg.stepCollect === 'function' &&
+      (typeof this.gg.decodePath !== 'function' || this.gg.decodePath(this.ctx) === 1);
+    if (queued) {
       // The same loop with one step queued ahead: step k + 1 is submitted
       // before step k's id reaches the host (it takes that id on the device),
       // so the GPU runs the steps back to back. The ids, the yields and the

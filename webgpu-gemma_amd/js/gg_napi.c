@@ -322,6 +322,21 @@ static napi_value Destroy(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* decodePath(ctx): 1 while forward passes run on the persistent kernel
+ * (stepSubmit queues a launch and returns), 0 on the graph path (stepSubmit
+ * runs the step before it returns; gg_decode_path). */
+static napi_value DecodePath(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  gg_ctx* ctx = get_ctx(env, argv[0]);
+  if (!ctx) return NULL;
+  int p = gg_decode_path(ctx);
+  if (p < 0) return throw_rc(env, ctx, p);
+  napi_value r;
+  CHECK(env, napi_create_int32(env, p, &r));
+  return r;
+}
+
 /* stepSubmit(ctx, id, pos, T, topP, rep, u): queues a step and returns
  * without waiting (gg_step_submit); stepCollect awaits it. */
 static napi_value StepSubmit(napi_env env, napi_callback_info info) {
@@ -517,7 +532,7 @@ static napi_value Init(napi_env env, napi_value exports) {
     napi_callback cb;
   } fns[] = {{"create", Create},   {"upload", Upload},         {"finalize", Finalize}, {"prefill", Prefill},
              {"select", Select},   {"step", Step},             {"stepSubmit", StepSubmit},
-             {"stepCollect", StepCollect}, {"penaltyReset", PenaltyReset},
+             {"stepCollect", StepCollect}, {"decodePath", DecodePath}, {"penaltyReset", PenaltyReset},
              {"penaltyAdd", PenaltyAdd}, {"resetKV", ResetKV}, {"read", Read},         {"destroy", Destroy}};
   for (size_t i = 0; i < sizeof(fns) / sizeof(fns[0]); ++i) {
     napi_value f;
