@@ -24,7 +24,8 @@ extern "C" {
 #define GG_ERR_INVALID (-1)      /* bad argument, shape or state            */
 #define GG_ERR_NO_DEVICE (-2)    /* no HIP device / not gfx950 ("No WebGPU adapter found", engine.ts:125-127) */
 #define GG_ERR_HIP (-3)          /* HIP runtime error                       */
-#define GG_ERR_DEVICE_LOST (-4)  /* sticky fault; recreate the context ("WebGPU device lost", engine.ts:134-137,812,958) */
+#define GG_ERR_DEVICE_LOST (-4)  /* sticky fault (a HIP error that poisons the context); recreate the
+                                    context ("WebGPU device lost", engine.ts:134-137,812,958) */
 #define GG_ERR_MISSING (-5)      /* gg_finalize: a required tensor was never uploaded */
 #define GG_ERR_OOM (-6)          /* device allocation failed               */
 
@@ -136,7 +137,9 @@ int gg_step(gg_ctx* ctx, int32_t token, int32_t pos, const gg_sample* s, double 
  * collected and not used leaves its K/V row at `pos` and its id in the
  * penalty set; the next prefill at `pos` overwrites the row, and
  * gg_penalty_reset clears the set. Without the persistent decode kernel's
- * single-launch step, gg_step_submit runs the step before it returns. */
+ * single-launch step (gg_decode_path: GG_DECODE_GRAPH, or a vocabulary that
+ * is not a multiple of 16384), gg_step_submit runs the step before it
+ * returns. */
 int gg_step_submit(gg_ctx* ctx, int32_t token, int32_t pos, const gg_sample* s, double u);
 int gg_step_collect(gg_ctx* ctx, int32_t* out_token);
 
@@ -192,7 +195,20 @@ int gg_probe_overhead(gg_ctx* ctx, float* ms);
  * phase (133 per 1B token). Both compute the same functions; summation
  * orders differ. The environment variable GG_DECODE=graph selects the
  * graph path when gg_set_decode_path was not called. No counterpart in the
- * reference (engine.ts:735-802 encodes one dispatch per kernel). */
+ * reference (engine.ts:735-802 encodes one dispatch per kernel).
+ *
+ * The persistent kernel needs all 256 of its blocks resident at once. The
+ * persistent launches of all contexts of a process on one device run one at
+ * a time (each waits for the other contexts' latest one). Every hand-off wait
+ * inside the kernel is bounded (20 ms): if a launch's blocks could not all
+ * run together (CUs held by another process) or a hand-off stalled, the
+ * launch ends, the context switches to GG_DECODE_GRAPH for good and the call
+ * runs its work again there -- a token-by-token prefill, a step, or a
+ * pipelined step and the one queued behind it -- so it still returns the
+ * selection with GG_OK; gg_decode_path then reports GG_DECODE_GRAPH. With
+ * GG_DEC_COOP=1 in the environment at gg_finalize, direct persistent
+ * launches are cooperative launches instead (the runtime refuses a grid that
+ * cannot be resident; 4% slower per step on MI355X). */
 #define GG_DECODE_GRAPH 0
 #define GG_DECODE_FUSED 1
 int gg_set_decode_path(gg_ctx* ctx, int32_t path);   /* before gg_finalize */
@@ -238,9 +254,11 @@ int gg_select_logits(const float* logits, int32_t n, const uint32_t* seen_bitmap
                      int32_t* out_token, void* stream);
 
 /* gg_select_logits without a workspace argument and without any device
- * allocation: for callers that cannot allocate (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
- * the reference. The workspace is a static 67,840-byte device array, one
+ * allocation: for callers that cannot allocate (tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. It is
+ * not usable under HIP graph capture: it copies the sampling state from host
+ * memory and synchronizes the stream, and returns only once the selection
+ * has finished. The workspace is a static 67,840-byte device array, one
  * copy per GPU, held until the process ends; its address is looked up once
  * per device on the first call there. Every call on one GPU shares that
  * array: calls that overlap on one GPU (other streams or host threads) race.

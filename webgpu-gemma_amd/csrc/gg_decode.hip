@@ -209,6 +209,17 @@ __device__ __forceinline__ float red_row(const float (*red)[kDecMaxRows], int t)
   return r;
 }
 
+// The kernel arguments read through a pointer the compiler cannot follow
+// across loop iterations: fields used in a layer are loaded (s_load from the
+// kernarg segment) where the layer needs them instead of being kept live in
+// scalar registers across the whole layer loop, where most of them spilled.
+typedef __attribute__((address_space(4))) const DecodeArgs KArgs;
+__device__ __forceinline__ KArgs& kargs() {
+  uint64_t p = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *(KArgs*)p;
+}
+
 struct Smem {
   union {
     float4 xs4[kMaxK / 64 * kXPad / 4]; // GEMV input x (K <= 8192)
@@ -233,21 +244,17 @@ struct Smem {
 
 // Timeline stamp (profiling builds of a step only): thread 0 of each block
 // records s_memrealtime at event ev of layer l.
-__device__ __forceinline__ void stamp(const DecodeArgs& a, int b, int l, int ev) {
+template <class DA>
+__device__ __forceinline__ void stamp(const DA& a, int b, int l, int ev) {
   if (a.timeline && tidx() == 0)
     a.timeline[((size_t)b * a.L + l) * kDecEvents + ev] = __builtin_amdgcn_s_memrealtime();
 }
 
-// A block whose hand-off wait ran out (called by every thread of the block):
-// raises the launch's flags in mapped host memory and, when fewer than all
-// blocks of this launch have started (their arrival words lack this epoch),
-// records how many had: the launch was not co-resident.
-__device__ __forceinline__ void report_timeout(const DecodeArgs& a, uint32_t epoch) {
-  const int tid = tidx();
-  const bool here = __hip_atomic_load(a.arrive + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch + 1;
-  const int n = __syncthreads_count(here);
-  if (tid == 0) {
-    if (n < kDecBlocks) __hip_atomic_store(a.host_out + 2, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+// A block whose hand-off wait ran out: raises the launch's flags in mapped
+// host memory (the context then continues on the graph path).
+template <class DA>
+__device__ __forceinline__ void report_timeout(const DA& a) {
+  if (tidx() == 0) {
     __hip_atomic_store(a.host_out + 8 + a.out_slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(a.host_out + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
@@ -474,7 +481,8 @@ struct LayerView {
   const float* rope;
   int window;
 };
-__device__ __forceinline__ LayerView layer_view(const DecodeArgs& a, int l) {
+template <class DA>
+__device__ __forceinline__ LayerView layer_view(const DA& a, int l) {
   LayerView v;
   v.qkv = a.w_qkv + (size_t)l * a.st_qkv;
   v.o = a.w_o + (size_t)l * a.st_o;
@@ -488,11 +496,13 @@ __device__ __forceinline__ LayerView layer_view(const DecodeArgs& a, int l) {
   v.window = swa ? a.window : 0;
   return v;
 }
-__device__ __forceinline__ const float* norm_of(const DecodeArgs& a, const LayerView& v, int j) {
+template <class DA>
+__device__ __forceinline__ const float* norm_of(const DA& a, const LayerView& v, int j) {
   return v.norms + (size_t)j * a.norm_stride;
 }
 
-__device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, const LayerView& Ly, int l, int c,
+template <class DA>
+__device__ __forceinline__ bool attention_block(const DA& a, Smem& S, const LayerView& Ly, int l, int c,
                                                 int h, int pos, uint32_t tag, int nchunks) {
   const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
   const long long lim = a.spin_limit;
@@ -695,8 +705,8 @@ __device__ __forceinline__ bool attention_block(const DecodeArgs& a, Smem& S, co
 // threads 0..2 NC - 1 also poll the (m, l) words. Every thread forms the
 // head's max and l-sum in chunk order; wave g sums its chunks in order and
 // the four waves' sums are added in wave order.
-template <int NC>
-__device__ __forceinline__ bool merge_head_part(const DecodeArgs& a, Smem& S, int l, int h, int p, uint32_t tag) {
+template <int NC, class DA>
+__device__ __forceinline__ bool merge_head_part(const DA& a, Smem& S, int l, int h, int p, uint32_t tag) {
   constexpr int KC = NC / 4;
   const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
   const uint64_t* base = a.x_part + (size_t)h * kDecChunksG * kDecPart;
@@ -791,7 +801,8 @@ __device__ __forceinline__ void head_norm_rope(float* x, const float* w, const f
 // wave w polls and normalises q of head w; in the block whose chunk holds
 // pos, wave 1 also takes this token's k and wave 2 its v, and the block
 // stores both into the cache. Partial of head h at (h * kDecChunksL + c).
-__device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, const LayerView& Ly, int l, int c,
+template <class DA>
+__device__ __forceinline__ bool attention_long(const DA& a, Smem& S, const LayerView& Ly, int l, int c,
                                                int pos, uint32_t tag) {
   LongAttn& LA = *reinterpret_cast<LongAttn*>(S.xs4);
   const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
@@ -1007,7 +1018,8 @@ __device__ __forceinline__ bool attention_long(const DecodeArgs& a, Smem& S, con
 // Thread t polls chunk t's (m, l) and dim t % 16 of chunks t / 16 + 16 k;
 // sums run in a fixed order (per thread in k, then xor trees over the
 // wave's chunk groups and the four waves in order).
-__device__ __forceinline__ bool merge_long(const DecodeArgs& a, Smem& S, int l, int hs, uint32_t tag) {
+template <class DA>
+__device__ __forceinline__ bool merge_long(const DA& a, Smem& S, int l, int hs, uint32_t tag) {
   LongAttn& LA = *reinterpret_cast<LongAttn*>(S.xs4);
   const int tid = tidx(), lane = tid & 63, wv = tid >> 6;
   const int h = hs >> 4, s = hs & 15, g = tid >> 4, d = tid & 15;
@@ -1083,7 +1095,6 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   const int cur = args_in ? -1 : st->cursor;
   const int token = args_in ? (a.in_token >= 0 ? a.in_token : st->out_token) : cur < 0 ? st->token : a.tokens[cur];
   const uint32_t base = epoch * (uint32_t)(a.L + 2);
-  if (tid == 0) __hip_atomic_store(a.arrive + b, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
 
   const int Kq = H / 64;
@@ -1100,6 +1111,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
   }
 
   for (int l = 0; l < a.L; ++l) {
+    KArgs& a = kargs();
     const int tid = tidx(), b = bidx();
     const LayerView Ly = layer_view(a, l);
     const uint32_t tag = base + (uint32_t)l + 1;
@@ -1182,19 +1194,19 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       stamp(a, b, l, 2);
       if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
         // long span: every block takes a chunk of the four heads
-        if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a, epoch); return; }
+        if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
         stamp(a, b, l, 14);
       } else if (Ly.window == 0 && b < 64) {
         // full-attention layers: blocks [0, 64) also take chunks 16..31
         const int c = 16 + (b & 7) + 8 * (b >> 5), h = (b >> 3) & 3;
-        if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a, epoch); return; }
+        if (!attention_block(a, S, Ly, l, c, h, pos, tag, kDecChunksG)) { report_timeout(a); return; }
       }
       issue_ffn();
     } else if (LONG && Ly.window == 0 && pos >= kDecMaxCtx) {
       // ---- A, long span: chunk b of the four heads, then the merge ----
-      if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a, epoch); return; }
+      if (!attention_long(a, S, Ly, l, b, pos, tag)) { report_timeout(a); return; }
       stamp(a, b, l, 2);
-      if (!merge_long(a, S, l, b - kDecQBlocks, tag)) { report_timeout(a, epoch); return; }
+      if (!merge_long(a, S, l, b - kDecQBlocks, tag)) { report_timeout(a); return; }
       stamp(a, b, l, 3);
       issue_ffn();
     } else {
@@ -1203,14 +1215,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       const int c = (ab & 7) + 8 * (ab >> 5), h = (ab >> 3) & 3;
       const bool glob = Ly.window == 0;
       if (!attention_block(a, S, Ly, l, c, h, pos, tag, glob ? kDecChunksG : kDecChunks)) {
-        report_timeout(a, epoch);
+        report_timeout(a);
         return;
       }
       stamp(a, b, l, 2);
       if (c < 4) {
         const bool mok =
             glob ? merge_head_part<kDecChunksG>(a, S, l, h, c, tag) : merge_head_part<kDecChunks>(a, S, l, h, c, tag);
-        if (!mok) { report_timeout(a, epoch); return; }
+        if (!mok) { report_timeout(a); return; }
         stamp(a, b, l, 3);
       }
       if (l > 0 && defer) update_resid();
@@ -1224,7 +1236,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       mg_issue<8, 1>(Ly.o, a.QD / 64, a.kps_o, b * a.kps_o, a.kps_o, wo);
       zero_red(S.red);
       const bool ok = poll_to_xs<kAttnMaxQ * kHeadDim / NT>(S, a.x_attn, a.QD, tag, lim);
-      if (failed(S, ok)) { report_timeout(a, epoch); return; }
+      if (failed(S, ok)) { report_timeout(a); return; }
       stamp(a, b, l, 3);
       mg_dots<8, 1>(wo, (const float*)S.xs4, a.QD / 64, a.kps_o, b, b * a.kps_o, a.kps_o, S.red);
       __syncthreads();
@@ -1339,7 +1351,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       stamp(a, b, l, 11);
     }
     __syncthreads();
-    if (S.fail) { report_timeout(a, epoch); return; }
+    if (S.fail) { report_timeout(a); return; }
   }
 
   // ---- end of the pass: post-FFN norm + residual, output norm ----
@@ -1374,7 +1386,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
     soft_fail(S, ok);
     resid_norm<true>(S, dv, wpost, wout, H, a.eps, r);
     __syncthreads();
-    if (S.fail) { report_timeout(a, epoch); return; }
+    if (S.fail) { report_timeout(a); return; }
     if (b == 0) {
       const float* xs = (const float*)S.xs4;
 #pragma unroll
@@ -1491,7 +1503,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
       if (now_ - t0 > lim) { ok = false; break; }
     }
   }
-  if (failed(S, ok)) { report_timeout(a, epoch); return; }
+  if (failed(S, ok)) { report_timeout(a); return; }
   if (tid < 256) {
     a.top[2 * tid] = __float_as_uint(m);
     a.top[2 * tid + 1] = id;

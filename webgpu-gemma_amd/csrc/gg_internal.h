@@ -277,7 +277,6 @@ struct DecodeArgs {
   uint64_t* x_down;        // [2][kDecXW]: layer l's down output in row l & 1, so a block that
                            // polls layer l - 1's row late never finds it overwritten by layer l's
   uint64_t* x_cand;        // [256][2]: per vocab class (value, id)
-  uint32_t* arrive;        // [kDecBlocks]: block b stores epoch + 1 at its start (residency check on a timeout)
   // parity outputs
   float* hidden;
   float* normed;
@@ -287,8 +286,7 @@ struct DecodeArgs {
   float* logits;           // DEC_STEP: [V] class-major
   uint32_t* top;           // [256] x {f32 bits, id}
   uint32_t* seen;          // penalty bitmap
-  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag, [2] blocks a timed-out
-                           // block found started when fewer than all (0: all), [4..5] pipelined tokens,
+  int32_t* host_out;       // mapped host words: [0] token, [1] hand-off timeout flag, [4..5] pipelined tokens,
                            // [8 + out_slot] timeout flag of the launch that writes host_out[out_slot]
   long long spin_limit;    // s_memrealtime ticks (100 MHz) one hand-off may wait
   long long* timeline;     // optional [256][L][kDecEvents] s_memrealtime stamps (null: off)

@@ -10,6 +10,7 @@
 // async copy before each launch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -338,17 +339,15 @@ int persistent_end(gg_ctx* c) {
 constexpr int kRetry = 1;
 int fall_back_to_graphs(gg_ctx* c) {
   GG_TRY(sync(c, "persistent decode kernel"));
-  const int resident = c->h_out[2];
-  for (int i : {1, 2, 8, 12, 13}) c->h_out[i] = 0;
+  for (int i : {1, 8, 12, 13}) c->h_out[i] = 0;
   GG_HIP(c, hipMemsetAsync(c->xll, 0, c->xll_words * 8, c->stream));
   GG_HIP(c, hipMemsetAsync((char*)c->st + offsetof(DevState, epoch), 0, 4, c->stream));
   GG_TRY(sync(c, "hand-off reset"));
   c->dec_launches = 0;
   c->fused = c->fused_step = false;
   fence_unregister(c);
-  c->fused_why = resident > 0 ? "a persistent decode launch found only " + std::to_string(resident) +
-                                    " of its 256 blocks started (the GPU is shared); switched to the graph path"
-                              : "a hand-off of the persistent decode kernel timed out; switched to the graph path";
+  c->fused_why = "a hand-off of the persistent decode kernel timed out (its 256 blocks were not all resident at "
+                 "once, e.g. on a GPU shared with other work); switched to the graph path";
   return kRetry;
 }
 
@@ -1075,8 +1074,8 @@ int gg_finalize(gg_ctx* c) {
     // hand-off words; polled buffers hold kDecThreads * (words per thread)
     const size_t w_qkv = (size_t)c->NQKV, w_part = (size_t)kAttnMaxQ * kDecChunksL * kDecPart;
     const size_t w_attn = (size_t)kAttnMaxQ * kHeadDim, w_h = kDecXW, w_dpart = (size_t)(c->I / 32) * c->H;
-    const size_t w_cand = 512, w_arrive = kDecBlocks / 2;
-    c->xll_words = w_qkv + w_part + w_attn + 3 * w_h + w_dpart + w_cand + w_arrive;
+    const size_t w_cand = 512;
+    c->xll_words = w_qkv + w_part + w_attn + 3 * w_h + w_dpart + w_cand;
     GG_TRY(dalloc(c, &c->xll, c->xll_words * 8));
     GG_HIP(c, hipMemset(c->xll, 0, c->xll_words * 8));
     d.x_qkv = c->xll;
@@ -1086,7 +1085,6 @@ int gg_finalize(gg_ctx* c) {
     d.x_down = d.x_o + w_h;   // two rows, by layer parity
     d.x_dpart = d.x_down + 2 * w_h;
     d.x_cand = d.x_dpart + w_dpart;
-    d.arrive = (uint32_t*)(d.x_cand + w_cand);
     d.w_qkv = c->s_qkv;
     d.w_o = c->s_o;
     d.w_guf = c->s_guf;
