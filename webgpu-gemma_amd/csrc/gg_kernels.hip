@@ -1168,14 +1168,16 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
 // chunks' (m, l, O) (maxima in log2 units, as k_attn_pf keeps them), one
 // block per (row, query head), thread = head dim.
 __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
-  const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nq = a.n_q;
+  // one block per prompt row: wave h merges head h, lane l dims 4 l .. 4 l + 3
+  // (16-byte loads of each chunk's o); the same per-element sums, in chunk
+  // order, as one thread per dim
+  const int row = blockIdx.x, tid = threadIdx.x, nq = a.n_q, h = tid >> 6, d4 = tid & 63;
   int klo, khi, nkc;
   pf_tile_span(a, row / kPfRows, &klo, &khi, &nkc);
-  if (nkc == 1) return;
+  if (nkc == 1 || h >= nq) return;
   const float* pr = a.part + (size_t)row * kPrefillChunks * nq * (2 + kHeadDim);
   // chunks in groups of four, each group's loads issued together (clamped
-  // indices; a group's chunks past nkc are skipped in the sums); the sums run
-  // in chunk order
+  // indices; a group's chunks past nkc are skipped in the sums)
   constexpr int G = 4;
   float M = -INFINITY;
   for (int c0 = 0; c0 < nkc; c0 += G) {
@@ -1186,27 +1188,38 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
     for (int j = 0; j < G; ++j)
       if (c0 + j < nkc) M = fmaxf(M, m[j]);
   }
-  float L = 0.f, O = 0.f;
+  float L = 0.f;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int c0 = 0; c0 < nkc; c0 += G) {
-    float m[G], l[G], o[G];
+    float m[G], l[G];
+    float4 o[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       const float* pc = pr + (min(c0 + j, nkc - 1) * nq + h) * (2 + kHeadDim);
       m[j] = pc[0];
       l[j] = pc[1];
-      o[j] = pc[2 + tid];
+      // a partial's o starts 2 floats into its 258-float record: 8-byte aligned
+      const float2 lo2 = *(const float2*)(pc + 2 + 4 * d4), hi2 = *(const float2*)(pc + 4 + 4 * d4);
+      o[j] = make_float4(lo2.x, lo2.y, hi2.x, hi2.y);
     }
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       if (c0 + j < nkc) {
         const float f = m[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[j] - M);
         L = fmaf(f, l[j], L);
-        O = fmaf(f, o[j], O);
+        O.x = fmaf(f, o[j].x, O.x);
+        O.y = fmaf(f, o[j].y, O.y);
+        O.z = fmaf(f, o[j].z, O.z);
+        O.w = fmaf(f, o[j].w, O.w);
       }
     }
   }
-  const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + tid;
-  split_bf16(O / L, &a.pf_out[e], &a.pf_out[(size_t)a.pf_rows * nq * kHeadDim + e]);
+  const size_t e = (size_t)row * nq * kHeadDim + h * kHeadDim + 4 * d4;
+  const size_t lo = (size_t)a.pf_rows * nq * kHeadDim;
+  split_bf16(O.x / L, &a.pf_out[e], &a.pf_out[lo + e]);
+  split_bf16(O.y / L, &a.pf_out[e + 1], &a.pf_out[lo + e + 1]);
+  split_bf16(O.z / L, &a.pf_out[e + 2], &a.pf_out[lo + e + 2]);
+  split_bf16(O.w / L, &a.pf_out[e + 3], &a.pf_out[lo + e + 3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1441,30 +1454,50 @@ __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
 // One block per prompt row: RMSNorm + NEOX RoPE of the key head (into the
 // cache, with v) and of every query head, the latter in place in the QKV
 // rows for the attention kernel (fusedPerHeadNormRope, shaders.ts:420-467).
-__global__ __launch_bounds__(256) void k_rows_kv(RowArgs a) {
-  __shared__ float sh4[4];
-  __shared__ float kk[kHeadDim];
-  const int row = blockIdx.x, tid = threadIdx.x;
+__global__ __launch_bounds__(320) void k_rows_kv(RowArgs a) {
+  // wave w < n_q: query head w of the row, in place; wave n_q: the key head
+  // (into the cache) and the value row. Lane l holds dims l + 64 j, so the
+  // NEOX pairs (i, i + 128) are its own j and j + 2, and the head's sum of
+  // squares is one wave reduction: no LDS, no barrier
+  const int row = blockIdx.x, wv = threadIdx.x >> 6, lane = threadIdx.x & 63, nq = a.n_q;
+  if (wv > nq) return;
   const int pos = a.pf_start + row;
-  float* qrow = const_cast<float*>(a.qkv) + (size_t)row * (a.n_q * kHeadDim + 2 * kHeadDim);
-  const float* q = qrow + a.n_q * kHeadDim;
-  const float k = q[tid], v = q[kHeadDim + tid], w = a.k_norm[tid];
+  float* qrow = const_cast<float*>(a.qkv) + (size_t)row * (nq * kHeadDim + 2 * kHeadDim);
+  float* src = qrow + wv * kHeadDim;   // wave nq: the key head
+  const float* w = wv < nq ? a.q_norm : a.k_norm;
   const float* rt = a.rope + (size_t)pos * kHeadDim;
-  const float cs = rt[tid & 127], sn = rt[128 + (tid & 127)];
-  auto norm_rope = [&](float x, float wt) {
-    const float ri = rsq(block_sum256(x * x, sh4) / (float)kHeadDim + a.eps);
-    kk[tid] = (x * wt) * ri;
-    __syncthreads();
-    const float out = tid < 128 ? kk[tid] * cs - kk[tid + 128] * sn : kk[tid - 128] * sn + kk[tid] * cs;
-    __syncthreads();
-    return out;
-  };
-  a.k_cache[(size_t)pos * kHeadDim + tid] = norm_rope(k, w);
-  a.v_cache[(size_t)pos * kHeadDim + tid] = v;
-  const float wq = a.q_norm[tid];
-  for (int h = 0; h < a.n_q; ++h) {
-    const float x = qrow[h * kHeadDim + tid];
-    qrow[h * kHeadDim + tid] = norm_rope(x, wq);
+  float x[4], nw[4], cs[2], sn[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[j] = src[lane + 64 * j];
+    nw[j] = w[lane + 64 * j];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cs[j] = rt[lane + 64 * j];
+    sn[j] = rt[kHeadDim / 2 + lane + 64 * j];
+  }
+  float v[4];
+  if (wv == nq) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = src[kHeadDim + lane + 64 * j];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss = fmaf(x[j], x[j], ss);
+  const float ri = rsq(wave_sum_dpp(ss) / (float)kHeadDim + a.eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = (x[j] * nw[j]) * ri;
+  float* dst = wv < nq ? src : a.k_cache + (size_t)pos * kHeadDim;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float x0 = x[j], x1 = x[j + 2];
+    dst[lane + 64 * j] = x0 * cs[j] - x1 * sn[j];
+    dst[lane + 64 * j + 128] = x0 * sn[j] + x1 * cs[j];
+  }
+  if (wv == nq) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a.v_cache[(size_t)pos * kHeadDim + lane + 64 * j] = v[j];
   }
 }
 
@@ -1764,7 +1797,7 @@ int launch_prefill_attention(const AttnArgs& a, int M, void* stream) {
   const int nkc = (span + a.pf_chunk - 1) / a.pf_chunk;
   if (nkc > kPrefillChunks) return (int)hipErrorInvalidValue;   // `part` holds kPrefillChunks per row
   hipLaunchKernelGGL(k_attn_pf, dim3(nkc, (M + kPfRows - 1) / kPfRows), dim3(512), 0, (hipStream_t)stream, a);
-  if (nkc > 1) hipLaunchKernelGGL(k_attn_pf_merge, dim3(M, a.n_q), dim3(256), 0, (hipStream_t)stream, a);
+  if (nkc > 1) hipLaunchKernelGGL(k_attn_pf_merge, dim3(M), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
@@ -1867,7 +1900,8 @@ int launch_rows_resid(const RowArgs& a, void* stream) {
 
 int launch_rows_kv(const RowArgs& a, void* stream) {
   if (a.M < 1) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rows_kv, dim3(a.M), dim3(256), 0, (hipStream_t)stream, a);
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_kv, dim3(a.M), dim3(64 * (a.n_q + 1)), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
