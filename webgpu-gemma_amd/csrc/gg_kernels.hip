@@ -1413,42 +1413,87 @@ __global__ __launch_bounds__(256) void k_rows_embed(RowArgs a) {
 }
 
 __global__ __launch_bounds__(256) void k_rows_resid(RowArgs a) {
-  __shared__ float sh4[4];
-  const int row = blockIdx.x, tid = threadIdx.x, H = a.H;
-  const int n = (H - tid + 255) / 256;
-  const size_t o = (size_t)row * H;
-  float v[8], rs[8], wq[8], pv[kGemmMaxSlices - 1][8];
-  // every plane's loads are issued before the sums (planes of a K split)
+  // one wave per prompt row, four rows per block: lane l holds float4s
+  // l + 64 k of the row, so both sums of squares are wave reductions (no
+  // LDS, no barrier); every load of the row is issued before the sums
+  constexpr int KF = 2048 / 4 / 64;   // float4s per lane at the largest hidden size
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6), H = a.H;
+  if (row >= a.M) return;
+  const int F4 = H / 4;
+  const size_t o4 = (size_t)row * F4;
+  const float4* pre = (const float4*)a.pre;
+  const float4* res = (const float4*)a.res;
+  const float4* wpost = (const float4*)a.w_post;
+  const float4* wpre = (const float4*)a.w_pre;
+  const size_t ps4 = a.pre_stride / 4;
+  float4 v[KF], rs[KF], wq[KF];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < n) {
-      v[i] = a.pre[o + tid + 256 * i];
+  for (int k = 0; k < KF; ++k) {
+    const int f = lane + 64 * k;
+    if (f < F4) {
+      v[k] = pre[o4 + f];
+      float4 pv[kGemmMaxSlices - 1];
 #pragma unroll
       for (int p = 1; p < kGemmMaxSlices; ++p)
-        if (p < a.pre_planes) pv[p - 1][i] = a.pre[p * a.pre_stride + o + tid + 256 * i];
-      rs[i] = a.res[o + tid + 256 * i];
-      wq[i] = a.w_post[tid + 256 * i];
-    }
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < n) {
+        if (p < a.pre_planes) pv[p - 1] = pre[p * ps4 + o4 + f];
+      rs[k] = res[o4 + f];
+      wq[k] = wpost[f];
+      // K slices of the previous GEMM, added in slice order
 #pragma unroll
       for (int p = 1; p < kGemmMaxSlices; ++p)
-        if (p < a.pre_planes) v[i] += pv[p - 1][i];
+        if (p < a.pre_planes) {
+          v[k].x += pv[p - 1].x;
+          v[k].y += pv[p - 1].y;
+          v[k].z += pv[p - 1].z;
+          v[k].w += pv[p - 1].w;
+        }
     }
+  }
   float s1 = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < n) s1 = fmaf(v[i], v[i], s1);
-  const float ri1 = rsq(block_sum256(s1, sh4) / (float)H + a.eps);
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < n) {
-      v[i] = rs[i] + (v[i] * wq[i]) * ri1;
-      a.res_out[o + tid + 256 * i] = v[i];
-      if (a.last_hidden && row == a.M - 1) a.last_hidden[tid + 256 * i] = v[i];
+  for (int k = 0; k < KF; ++k)
+    if (lane + 64 * k < F4) {
+      s1 = fmaf(v[k].x, v[k].x, s1);
+      s1 = fmaf(v[k].y, v[k].y, s1);
+      s1 = fmaf(v[k].z, v[k].z, s1);
+      s1 = fmaf(v[k].w, v[k].w, s1);
     }
-  row_norm_out(v, a.w_pre, H, a.eps, a.x_out + o, (size_t)a.M * H, sh4, n);
+  const float ri1 = rsq(wave_sum_dpp(s1) / (float)H + a.eps);
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < KF; ++k) {
+    const int f = lane + 64 * k;
+    if (f < F4) {
+      float4 r;
+      r.x = rs[k].x + (v[k].x * wq[k].x) * ri1;
+      r.y = rs[k].y + (v[k].y * wq[k].y) * ri1;
+      r.z = rs[k].z + (v[k].z * wq[k].z) * ri1;
+      r.w = rs[k].w + (v[k].w * wq[k].w) * ri1;
+      ((float4*)a.res_out)[o4 + f] = r;
+      if (a.last_hidden && row == a.M - 1) ((float4*)a.last_hidden)[f] = r;
+      v[k] = r;
+      ss = fmaf(r.x, r.x, ss);
+      ss = fmaf(r.y, r.y, ss);
+      ss = fmaf(r.z, r.z, ss);
+      ss = fmaf(r.w, r.w, ss);
+    }
+  }
+  const float ri = rsq(wave_sum_dpp(ss) / (float)H + a.eps);
+  const size_t plane = (size_t)a.M * H;
+#pragma unroll
+  for (int k = 0; k < KF; ++k) {
+    const int f = lane + 64 * k;
+    if (f < F4) {
+      const float4 w = wpre[f];
+      const float y[4] = {(v[k].x * w.x) * ri, (v[k].y * w.y) * ri, (v[k].z * w.z) * ri, (v[k].w * w.w) * ri};
+      uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) split_bf16(y[j], &hi[j], &lo[j]);
+      const size_t e = (size_t)row * H + 4 * f;
+      *(uint2*)(a.x_out + e) = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+      *(uint2*)(a.x_out + plane + e) = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+    }
+  }
 }
 
 // One block per prompt row: RMSNorm + NEOX RoPE of the key head (into the
@@ -1894,7 +1939,8 @@ int launch_rows_embed(const RowArgs& a, void* stream) {
 
 int launch_rows_resid(const RowArgs& a, void* stream) {
   if (a.H > 2048 || a.M < 1) return (int)hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rows_resid, dim3(a.M), dim3(256), 0, (hipStream_t)stream, a);
+  if (a.H % 4 || a.pre_stride % 4) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_resid, dim3((a.M + 3) / 4), dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 
