@@ -347,6 +347,7 @@ int launch_rows_embed(const RowArgs& a, void* stream);
 int launch_rows_resid(const RowArgs& a, void* stream);
 int launch_rows_kv(const RowArgs& a, void* stream);
 constexpr int kGemmMaxSlices = 4;   // K slices of a prefill GEMM (summed by the consumer)
+constexpr int kQkvMaxSlices = 2;    // ... of the QKV GEMM (summed by k_rows_kv)
 constexpr int kPrefillChunks = 16;   // key chunks per query tile in the batched prefill attention
 constexpr int kPrefillMinChunk = 160;
 // Longest key span of a 32-row query tile of a prefill of M rows at `start`.

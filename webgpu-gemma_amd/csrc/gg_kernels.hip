@@ -1511,12 +1511,18 @@ __global__ __launch_bounds__(320) void k_rows_kv(RowArgs a) {
   float* src = qrow + wv * kHeadDim;   // wave nq: the key head
   const float* w = wv < nq ? a.q_norm : a.k_norm;
   const float* rt = a.rope + (size_t)pos * kHeadDim;
+  // the QKV GEMM's K slices (pre_planes of them, pre_stride floats apart)
+  // are added in slice order; the sum stays in slice 0
+  const int ns = a.pre_planes > 1 ? a.pre_planes : 1;
   float x[4], nw[4], cs[2], sn[2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     x[j] = src[lane + 64 * j];
     nw[j] = w[lane + 64 * j];
   }
+  for (int p = 1; p < ns; ++p)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] += src[p * a.pre_stride + lane + 64 * j];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     cs[j] = rt[lane + 64 * j];
@@ -1526,6 +1532,9 @@ __global__ __launch_bounds__(320) void k_rows_kv(RowArgs a) {
   if (wv == nq) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = src[kHeadDim + lane + 64 * j];
+    for (int p = 1; p < ns; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += src[p * a.pre_stride + kHeadDim + lane + 64 * j];
   }
   float ss = 0.f;
 #pragma unroll
@@ -1946,7 +1955,9 @@ int launch_rows_resid(const RowArgs& a, void* stream) {
 
 int launch_rows_kv(const RowArgs& a, void* stream) {
   if (a.M < 1) return (int)hipErrorInvalidValue;
-  if (a.n_q < 1 || a.n_q > kAttnMaxQ) return (int)hipErrorInvalidValue;
+  if (a.n_q < 1 || a.n_q > kAttnMaxQ || a.pre_planes > kQkvMaxSlices ||
+      (a.pre_planes > 1 && a.pre_stride < (size_t)a.M * (a.n_q + 2) * kHeadDim))
+    return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(k_rows_kv, dim3(a.M), dim3(64 * (a.n_q + 1)), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }

@@ -670,9 +670,12 @@ int prefill_slice(gg_ctx* c, const int32_t* d_tokens, int M, int start) {
   for (int l = 0; l < c->L; ++l) {
     Layer& Ly = c->layers[l];
     const bool swa = is_swa(c->c, l);
-    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gemm_base(c->pf_xn, Ly.qkv_b, Ly.qkv_d, c->NQKV, c->H, M, c->pf_qkv, nullptr), s), "prefill qkv"));
+    const GemmArgs gq = gemm_base(c->pf_xn, Ly.qkv_b, Ly.qkv_d, c->NQKV, c->H, M, c->pf_qkv, nullptr, kQkvMaxSlices);
+    GG_TRY(launch_rc(c, launch_gemm(EPI_OUT, gq, s), "prefill qkv"));
     RowArgs kv{};
     kv.M = M;
+    kv.pre_planes = gq.ks;
+    kv.pre_stride = (size_t)M * c->NQKV;
     kv.eps = eps;
     kv.pf_start = start;
     kv.qkv = c->pf_qkv;
@@ -1010,7 +1013,7 @@ int gg_finalize(gg_ctx* c) {
     GG_TRY(dalloc(c, &c->pf_residual, MH));
     GG_TRY(dalloc(c, &c->pf_xn, MH));   // bf16 hi + lo planes: 4 bytes per element
     GG_TRY(dalloc(c, &c->pf_o, kGemmMaxSlices * MH));   // K slices of the O / down GEMMs
-    GG_TRY(dalloc(c, &c->pf_qkv, (size_t)M * c->NQKV * 4));
+    GG_TRY(dalloc(c, &c->pf_qkv, (size_t)kQkvMaxSlices * M * c->NQKV * 4));   // K slices of the QKV GEMM
     GG_TRY(dalloc(c, &c->pf_attn, (size_t)M * c->QD * 4));
     GG_TRY(dalloc(c, &c->pf_act, (size_t)M * c->I * 4));
     GG_TRY(dalloc(c, &c->pf_part, (size_t)M * kPrefillChunks * kAttnMaxQ * (2 + kHeadDim) * 4));
