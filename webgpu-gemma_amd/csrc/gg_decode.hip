@@ -115,6 +115,23 @@ __device__ __forceinline__ bool ll_wait(const uint64_t* src, int n, uint32_t tag
   }
 }
 
+// Four 16-byte device-scope loads (two LL words each: value, tag, value,
+// tag), waited for inside the same asm statement so that no result register
+// is read before its load has returned. Each 8-byte word is read whole, as
+// by ll_ld; the tag test per word keeps the hand-off valid word by word.
+__device__ __forceinline__ void ll_ld4x2(const uint64_t* p0, const uint64_t* p1, const uint64_t* p2,
+                                         const uint64_t* p3, u32x4 (&w)[4]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+      : "memory");
+}
+
 // v + v of lane ^ 8 / ^ 16 / ^ 32 in every lane, on DPP (row_ror:8) and the
 // gfx950 half-row / half-wave swaps (v_permlane16/32_swap) rather than
 // ds_bpermute: the same IEEE sums as a shuffle, at VALU latency.
@@ -1311,36 +1328,50 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
 
     // ---- R: down output rows 8 b .. 8 b + 7 = sum over the I / 32 partials ----
     if (b < a.g_down) {
-      // thread t: row j = t % 8, partials m = t / 8 + 32 k, so eight
-      // consecutive lanes read the eight rows of one partial (one 64-byte
-      // line); each thread sums its partials in increasing m, then a fixed
-      // xor tree over the wave's m slots and the four waves in order
-      constexpr int PR = (kDecMaxFBlocks + 31) / 32;
-      const int j = tid & 7, mt = tid >> 3;
-      const uint64_t* src = a.x_dpart + 8 * b + j;
+      // thread t: rows 2 jp, 2 jp + 1 (jp = t % 4) of partials m = t / 4 +
+      // 64 k, one 16-byte load (two LL words) each, so four consecutive
+      // lanes read the eight rows of one partial (one 64-byte line); each
+      // thread sums its partials in increasing m, then a fixed tree over the
+      // wave's m slots and the four waves in order
+      constexpr int PR = (kDecMaxFBlocks + 63) / 64;
+      static_assert(PR == 4, "the partial poll issues four 16-byte loads");
+      const int jp = tid & 3, mt = tid >> 2;
+      const uint64_t* src = a.x_dpart + 8 * b + 2 * jp;
       const long long t0 = __builtin_amdgcn_s_memrealtime();
-      float acc = 0.f;
+      float acc0 = 0.f, acc1 = 0.f;
       bool ok = true;
       for (;;) {
         const long long now_ = __builtin_amdgcn_s_memrealtime();   // in flight with the loads
-        uint64_t w[PR];
-#pragma unroll
-        for (int k = 0; k < PR; ++k) w[k] = ll_ld(src + (size_t)min(mt + 32 * k, a.g_f - 1) * H);
+        u32x4 w[PR];
+        ll_ld4x2(src + (size_t)min(mt, a.g_f - 1) * H, src + (size_t)min(mt + 64, a.g_f - 1) * H,
+                 src + (size_t)min(mt + 128, a.g_f - 1) * H, src + (size_t)min(mt + 192, a.g_f - 1) * H, w);
         bool good = true;
 #pragma unroll
-        for (int k = 0; k < PR; ++k) good &= (mt + 32 * k >= a.g_f) | ll_ok(w[k], tag);
+        for (int k = 0; k < PR; ++k) good &= (mt + 64 * k >= a.g_f) | ((w[k][1] == tag) & (w[k][3] == tag));
         if (good) {
 #pragma unroll
           for (int k = 0; k < PR; ++k)
-            if (mt + 32 * k < a.g_f) acc += ll_val(w[k]);
+            if (mt + 64 * k < a.g_f) {
+              acc0 += __uint_as_float(w[k][0]);
+              acc1 += __uint_as_float(w[k][2]);
+            }
           break;
         }
         if (now_ - t0 > lim) { ok = false; break; }
       }
       soft_fail(S, ok);
       stamp(a, b, l, 7);
-      acc = xor32_add(xor16_add(xor8_add(acc)));
-      if ((tid & 63) < 8) S.red[tid >> 6][j] = acc;
+      // lanes i, i + 4, i + 8, i + 12 of each 16-lane row (rotations by 8, then 4), then the half-rows and halves
+      acc0 += dpp_mov<0x128>(acc0);
+      acc1 += dpp_mov<0x128>(acc1);
+      acc0 += dpp_mov<0x124>(acc0);
+      acc1 += dpp_mov<0x124>(acc1);
+      acc0 = xor32_add(xor16_add(acc0));
+      acc1 = xor32_add(xor16_add(acc1));
+      if ((tid & 63) < 4) {
+        S.red[tid >> 6][2 * jp] = acc0;
+        S.red[tid >> 6][2 * jp + 1] = acc1;
+      }
       __syncthreads();
       if (tid < 8) {
         float sum = 0.f;
