@@ -905,9 +905,28 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t* hi, uint16_t* lo) 
   *lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
 
-constexpr int kPfRows = 32;   // query rows per block: two 16-row MFMA tiles
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+// The same split for two values at once, as packed bf16 pairs (element 0 in
+// the low half): one packed conversion for hi, hi widened back by a shift and
+// a mask, one packed conversion for lo.
+__device__ __forceinline__ void split2_bf16(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){x0, x1}, bf16x2));
+  const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){x0 - h0, x1 - h1}, bf16x2));
+}
+// bf16 hi / lo of four values as packed pairs
+__device__ __forceinline__ void split4_bf16(float x0, float x1, float x2, float x3, bf16x4& hi, bf16x4& lo) {
+  uint32_t h[2], l[2];
+  split2_bf16(x0, x1, h[0], l[0]);
+  split2_bf16(x2, x3, h[1], l[1]);
+  hi = __builtin_bit_cast(bf16x4, h);
+  lo = __builtin_bit_cast(bf16x4, l);
+}
+
+constexpr int kPfRows = 32;   // query rows per block: two 16-row MFMA tiles
 __device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
 }
@@ -963,9 +982,8 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int kr = 8 * i + wv;
       const float4 x = st[i];
-      const bf16x4 hi = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
-      const bf16x4 lo = {(__bf16)(x.x - (float)hi[0]), (__bf16)(x.y - (float)hi[1]), (__bf16)(x.z - (float)hi[2]),
-                         (__bf16)(x.w - (float)hi[3])};
+      bf16x4 hi, lo;
+      split4_bf16(x.x, x.y, x.z, x.w, hi, lo);
       const int o = kr * kHeadDim + 8 * ((lane >> 1) ^ kswz(kr)) + 4 * (lane & 1);
       *(bf16x4*)&Kh[o] = hi;
       *(bf16x4*)&Kl[o] = lo;
@@ -991,11 +1009,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       bf16x4 hi, lo;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        hi[i] = (__bf16)vv[i][e];
-        lo[i] = (__bf16)(vv[i][e] - (float)hi[i]);
-      }
+      split4_bf16(vv[0][e], vv[1][e], vv[2][e], vv[3][e], hi, lo);
       const int d = 4 * lane + e;
       const int o = d * kPfKeys + 8 * ((wv >> 1) ^ ((d >> 1) & 3)) + 4 * (wv & 1);
       *(bf16x4*)&Vh[o] = hi;
@@ -1022,11 +1036,11 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
   for (int t = 0; t < 8; ++t) {
     const float4 x0 = *(const float4*)(qp + 32 * t), x1 = *(const float4*)(qp + 32 * t + 4);
     const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    uint32_t h4[4], l4[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qh[t][e] = (__bf16)xs[e];
-      ql[t][e] = (__bf16)(xs[e] - (float)qh[t][e]);
-    }
+    for (int e = 0; e < 4; ++e) split2_bf16(xs[2 * e], xs[2 * e + 1], h4[e], l4[e]);
+    qh[t] = __builtin_bit_cast(bf16x8, h4);
+    ql[t] = __builtin_bit_cast(bf16x8, l4);
   }
   stage_k();
 
@@ -1113,14 +1127,13 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
       }
       // O += P V on bf16 MFMA: A = P (row l % 16, keys 8 g .. 8 g + 7 =
       // p[j][r] for key 8 g + 4 j + r), B = V^T rows; hi.hi, lo.hi, hi.lo
-      bf16x8 ph, pl;
+      uint32_t ph4[4], pl4[4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          ph[4 * j + r] = (__bf16)p[j][r];
-          pl[4 * j + r] = (__bf16)(p[j][r] - (float)ph[4 * j + r]);
-        }
+      for (int j = 0; j < 2; ++j) {
+        split2_bf16(p[j][0], p[j][1], ph4[2 * j], pl4[2 * j]);
+        split2_bf16(p[j][2], p[j][3], ph4[2 * j + 1], pl4[2 * j + 1]);
+      }
+      const bf16x8 ph = __builtin_bit_cast(bf16x8, ph4), pl = __builtin_bit_cast(bf16x8, pl4);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int d = 16 * i + c16;
