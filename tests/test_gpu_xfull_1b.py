@@ -1,4 +1,4 @@
-"""Gemma-3-1B at full size: a 2048-token seeded prompt,
+"""Gemma-3-1B at full size, greedy decode after a 2048-token context: a 2048-token seeded prompt,
 then 256 greedy tokens at batch 1, against the oracle run independently over
 the same 2048 positions (engine.ts:735-802 per token, 904-915 per step).
 The GPU fills its cache with the batched MFMA prefill and decodes on the
