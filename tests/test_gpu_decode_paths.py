@@ -363,3 +363,41 @@ def test_fused_step_ties_follow_the_reference_rule(gpu):
         v3, i3 = orc.topk256(L3)
         assert s == orc.sample_candidates(v3, i3, seen, 0.7, 0.9, 1.2, u), u
     e.close()
+
+
+@pytest.mark.parametrize("switch", ["GG_DEC_COOP", "GG_DEC_TIMELINE", "GG_NO_GRAPH"])
+def test_launch_switches_leave_results_unchanged(gpu, monkeypatch, switch):
+    """The launch switches a context reads at finalize change how kernels are
+    launched or observed, not what they compute: a cooperative launch of the
+    persistent kernel (GG_DEC_COOP=1), its phase stamps (GG_DEC_TIMELINE=1)
+    and direct launches instead of graphs (GG_NO_GRAPH=1) give the same
+    batched prefill, the same greedy and sampled ids and the same final
+    hidden state, bit for bit, as the default context on the 270M shape."""
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    tensors = synth.make_model(shape, seed=3)
+    prompt = synth.prompt_ids(100, seed=5, vocab=shape.vocab)
+
+    def run():
+        e = engine(shape, tensors, prefill_batch=64)
+        assert e.decode_path() == "fused"
+        e.prefill(prompt, 0)
+        tok = e.select()
+        ids, pos = [tok], len(prompt)
+        for i in range(12):
+            if i % 2:
+                tok = e.step(tok, pos, 0.8, 0.9, 1.3, 0.1 * i)
+            else:
+                tok = e.step(tok, pos)
+            ids.append(tok)
+            pos += 1
+        hidden = e.read(capi.READ_HIDDEN).copy()
+        e.close()
+        return ids, hidden
+
+    want_ids, want_hidden = run()
+    monkeypatch.setenv(switch, "1")
+    say(f"{switch}=1")
+    got_ids, got_hidden = run()
+    monkeypatch.delenv(switch)
+    assert got_ids == want_ids, (switch, got_ids, want_ids)
+    assert np.array_equal(got_hidden, want_hidden), (switch, rel(got_hidden, want_hidden))
