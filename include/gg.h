@@ -168,8 +168,11 @@ int gg_last_timing(gg_ctx* ctx, float* forward_ms, float* select_ms);
 /* Probe: before gg_finalize, name one kernel launch of the captured graphs
  * to bracket with HIP event-record nodes; after each gg_step / gg_select,
  * gg_probe_elapsed returns that launch's device time in milliseconds. Used by
- * the benchmark to time the dominant kernel inside the timed loop. No
- * counterpart in the reference (WebGPU has no per-dispatch timestamps in
+ * the benchmark to time the dominant kernel inside the timed loop. Where the
+ * HIP runtime of the process does not take external event records into a
+ * stream capture, the probed context launches the same kernels directly
+ * (as with GG_NO_GRAPH=1) and brackets the launch with ordinary records.
+ * No counterpart in the reference (WebGPU has no per-dispatch timestamps in
  * src/). */
 #define GG_PROBE_NONE 0
 #define GG_PROBE_QKV 1       /* fused QKV GEMV of layer `layer`           */

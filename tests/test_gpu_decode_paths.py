@@ -401,3 +401,55 @@ def test_launch_switches_leave_results_unchanged(gpu, monkeypatch, switch):
     monkeypatch.delenv(switch)
     assert got_ids == want_ids, (switch, got_ids, want_ids)
     assert np.array_equal(got_hidden, want_hidden), (switch, rel(got_hidden, want_hidden))
+
+
+def test_profiling_probes_and_timeline(gpu, monkeypatch):
+    """The profiling entry points report plausible device times and stamps
+    without changing what a step computes: on the graph path a probe on one
+    layer's gate/up GEMV (gg_set_probe) gives an elapsed time above its empty
+    event bracket and below the step's own time, with the same ids as an
+    unprobed context; on the persistent path GG_DEC_TIMELINE=1 fills every
+    (block, layer) start stamp (gg_decode_timeline), in increasing layer order
+    within each block."""
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    tensors = synth.make_model(shape, seed=4)
+    prompt = synth.prompt_ids(40, seed=6, vocab=shape.vocab)
+
+    def steps(e, n=6):
+        e.prefill(prompt, 0)
+        tok = e.select()
+        ids, pos = [tok], len(prompt)
+        for _ in range(n):
+            tok = e.step(tok, pos)
+            ids.append(tok)
+            pos += 1
+        return ids
+
+    plain = engine(shape, tensors, "graph")
+    want = steps(plain)
+    plain.close()
+
+    e = capi.Engine(shape.gg_config())
+    e.set_decode_path("graph")
+    e.set_probe("gate_up", 3)
+    e.upload_model(tensors)
+    e.finalize()
+    e.set_timing(True)
+    assert steps(e) == want
+    elapsed, overhead = e.probe_elapsed_ms(), e.probe_overhead_ms()
+    fwd_ms, _ = e.last_timing()
+    say(f"probe {elapsed * 1e3:.2f} us, bracket {overhead * 1e3:.2f} us, forward {fwd_ms * 1e3:.1f} us")
+    assert 0.0 <= overhead < elapsed < fwd_ms, (overhead, elapsed, fwd_ms)
+    e.close()
+
+    monkeypatch.setenv("GG_DEC_TIMELINE", "1")
+    e = engine(shape, tensors)
+    monkeypatch.delenv("GG_DEC_TIMELINE")
+    assert e.decode_path() == "fused"
+    steps(e, 2)
+    tl = e.decode_timeline()
+    e.close()
+    assert tl.shape == (256, shape.layers, 16)
+    start = tl[:, :, 0]
+    assert (start > 0).all()
+    assert (np.diff(start, axis=1) > 0).all()

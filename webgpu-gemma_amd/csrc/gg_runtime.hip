@@ -157,6 +157,8 @@ struct gg_ctx {
   long long* timeline = nullptr;      // GG_DEC_TIMELINE=1: phase stamps of the last launch
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int probe_kind = GG_PROBE_NONE, probe_layer = 0;
+  hipError_t probe_err = hipSuccess;  // first failed probe event record of a capture
+  bool capturing = false;             // a graph capture of c->stream is in progress
   hipEvent_t probe_ev[4] = {nullptr, nullptr, nullptr, nullptr};   // kernel bracket [0, 1], empty bracket [2, 3]
   bool probe_done = false;
   bool finalized = false, lost = false, timed = false, probed = false;
@@ -232,18 +234,31 @@ int check_idle(gg_ctx* c) {
 }
 
 // Bracket a launch with external event-record nodes when it is the probe.
+// A failed record is kept in probe_err (capture reports it) and cleared from
+// the runtime's last-error state, so the bracketed launch's status stays its
+// own.
 struct ProbeScope {
   gg_ctx* c;
   bool on;
   ProbeScope(gg_ctx* c_, int kind, int layer) : c(c_), on(c_->probe_kind == kind && (layer < 0 || c_->probe_layer == layer)) {
     if (on) {
-      (void)hipEventRecordWithFlags(c->probe_ev[2], c->stream, hipEventRecordExternal);
-      (void)hipEventRecordWithFlags(c->probe_ev[3], c->stream, hipEventRecordExternal);
-      (void)hipEventRecordWithFlags(c->probe_ev[0], c->stream, hipEventRecordExternal);
+      record(c->probe_ev[2]);
+      record(c->probe_ev[3]);
+      record(c->probe_ev[0]);
+    }
+  }
+  void record(hipEvent_t e) {
+    // inside a capture an external record becomes a record node of the
+    // graph; on direct launches it is an ordinary record
+    const hipError_t r =
+        c->capturing ? hipEventRecordWithFlags(e, c->stream, hipEventRecordExternal) : hipEventRecord(e, c->stream);
+    if (r != hipSuccess) {
+      if (c->probe_err == hipSuccess) c->probe_err = r;
+      (void)hipGetLastError();
     }
   }
   ~ProbeScope() {
-    if (on) (void)hipEventRecordWithFlags(c->probe_ev[1], c->stream, hipEventRecordExternal);
+    if (on) record(c->probe_ev[1]);
   }
 };
 
@@ -519,7 +534,9 @@ int record_select(gg_ctx* c) { return record_select_impl(c, false); }
 
 int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
   GG_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
+  c->capturing = true;
   int rc = rec(c);
+  c->capturing = false;
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(c->stream, &g);
   if (rc != GG_OK) {
@@ -527,6 +544,12 @@ int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
     return rc;
   }
   if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
+  if (c->probe_err != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    const hipError_t pe = c->probe_err;
+    c->probe_err = hipSuccess;
+    return hip_fail(c, pe, "probe event record");
+  }
   e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
   if (e != hipSuccess) return hip_fail(c, e, "hipGraphInstantiate");
@@ -534,6 +557,21 @@ int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
 }
 
 int push_state(gg_ctx* c, size_t from, size_t to);
+
+// Whether this runtime takes an external event record into a stream capture
+// (a throw-away capture of one record of the probe's first event).
+bool external_records_capture(gg_ctx* c) {
+  if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const hipError_t r = hipEventRecordWithFlags(c->probe_ev[0], c->stream, hipEventRecordExternal);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (g) (void)hipGraphDestroy(g);
+  (void)hipGetLastError();
+  return r == hipSuccess && e == hipSuccess;
+}
 
 // One decode step as a single graph: the DevState upload (a memcpy node
 // that reads the pinned host copy when the graph runs), the forward pass and
@@ -964,6 +1002,10 @@ int gg_finalize(gg_ctx* c) {
   if (!c) return GG_ERR_INVALID;
   if (c->lost) return set_err(c, GG_ERR_DEVICE_LOST, "device lost");
   if (c->finalized) return GG_OK;
+  // the launches below read the runtime's last error as their status: drop
+  // one that an earlier, checked-and-ignored call of this thread left (the
+  // teardown of another context, for instance)
+  (void)hipGetLastError();
   if (!c->have_embd) return set_err(c, GG_ERR_MISSING, "missing token_embd.weight");
   if (!c->have_out_norm) return set_err(c, GG_ERR_MISSING, "missing output_norm.weight");
   for (int l = 0; l < c->L; ++l)
@@ -1162,6 +1204,11 @@ int gg_finalize(gg_ctx* c) {
 
   const char* ng = getenv("GG_NO_GRAPH");
   c->use_graphs = !(ng && ng[0] == '1');
+  // a probe needs external event-record nodes in the captured graphs; a HIP
+  // runtime that refuses them (the ROCm 7.0 runtime a process may already
+  // have loaded under the same soname rejects them as an invalid value) gets
+  // the same kernels launched directly, bracketed by ordinary event records
+  if (c->use_graphs && c->probe_kind != GG_PROBE_NONE && !external_records_capture(c)) c->use_graphs = false;
   if (c->use_graphs) {
     GG_TRY(capture(c, record_forward, &c->g_fwd));
     GG_TRY(capture(c, record_select, &c->g_sel));
@@ -1557,6 +1604,7 @@ void gg_destroy(gg_ctx* c) {
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
+  (void)hipGetLastError();   // teardown errors are not the next call's
 }
 
 // ---- kernel-level entry points --------------------------------------------
