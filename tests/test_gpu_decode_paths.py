@@ -406,11 +406,11 @@ def test_launch_switches_leave_results_unchanged(gpu, monkeypatch, switch):
 def test_profiling_probes_and_timeline(gpu, monkeypatch):
     """The profiling entry points report plausible device times and stamps
     without changing what a step computes: on the graph path a probe on one
-    layer's gate/up GEMV (gg_set_probe) gives an elapsed time above its empty
-    event bracket and below the step's own time, with the same ids as an
-    unprobed context; on the persistent path GG_DEC_TIMELINE=1 fills every
-    (block, layer) start stamp (gg_decode_timeline), in increasing layer order
-    within each block."""
+    layer's gate/up GEMV (gg_set_probe) gives an elapsed time below the
+    step's own forward time (an empty bracket of its own is reported beside
+    it), with the same ids as an unprobed context; on the persistent path
+    GG_DEC_TIMELINE=1 fills every (block, layer) start stamp
+    (gg_decode_timeline), in increasing layer order within each block."""
     shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
     tensors = synth.make_model(shape, seed=4)
     prompt = synth.prompt_ids(40, seed=6, vocab=shape.vocab)
@@ -439,7 +439,9 @@ def test_profiling_probes_and_timeline(gpu, monkeypatch):
     elapsed, overhead = e.probe_elapsed_ms(), e.probe_overhead_ms()
     fwd_ms, _ = e.last_timing()
     say(f"probe {elapsed * 1e3:.2f} us, bracket {overhead * 1e3:.2f} us, forward {fwd_ms * 1e3:.1f} us")
-    assert 0.0 <= overhead < elapsed < fwd_ms, (overhead, elapsed, fwd_ms)
+    # on direct launches the empty bracket can span a host dispatch gap, so
+    # only the probed launch is bounded by the forward time
+    assert 0.0 < elapsed < fwd_ms and overhead >= 0.0, (overhead, elapsed, fwd_ms)
     e.close()
 
     monkeypatch.setenv("GG_DEC_TIMELINE", "1")
