@@ -455,3 +455,58 @@ def test_profiling_probes_and_timeline(gpu, monkeypatch):
     start = tl[:, :, 0]
     assert (start > 0).all()
     assert (np.diff(start, axis=1) > 0).all()
+
+
+def test_invalid_calls_are_refused_and_leave_the_context_usable(gpu, tiny_model):
+    """Arguments and call orders the C-ABI refuses: each returns its error
+    code (GG_ERR_INVALID, or GG_ERR_MISSING for an incomplete model) and
+    changes nothing, so the same context then prefills and decodes exactly
+    as a fresh one (the reference throws for the same misuse and keeps the
+    engine, engine.ts:923-1031)."""
+    shape = synth.TINY.gemma3_mode(window=7)
+    V, L, ctx = shape.vocab, shape.layers, shape.gg_config().context_length
+    prompt = synth.prompt_ids(9, seed=11, vocab=V)
+
+    def refused(code, fn, *args, **kw):
+        with pytest.raises(capi.GGError) as ex:
+            fn(*args, **kw)
+        assert ex.value.code == code, (fn.__name__, ex.value.code, str(ex.value))
+
+    fresh = engine(shape, tiny_model, prefill_batch=4)
+    fresh.prefill(prompt, 0)
+    want = [fresh.select()]
+    for k in range(5):
+        want.append(fresh.step(want[-1], len(prompt) + k))
+    fresh.close()
+
+    e = engine(shape, tiny_model, prefill_batch=4)
+    inv = capi.GG_ERR_INVALID
+    refused(inv, e.step_submit, -1, 0)                        # no id selected yet
+    refused(inv, e.step_collect)                              # nothing outstanding
+    refused(inv, e.prefill, [0, V], 0)                        # token id out of range
+    refused(inv, e.prefill, prompt, ctx - 3)                  # range past the context
+    refused(inv, e.read, 99, count=4)                         # unknown target
+    refused(inv, e.read, capi.READ_LAYER_HIDDEN, layer=L)     # layer out of range
+    refused(inv, e.set_decode_path, "graph")                  # after finalize
+    refused(inv, e.set_probe, "qkv", 0)                       # after finalize
+    refused(inv, e.probe_elapsed_ms)                          # no probe set
+    refused(inv, e.decode_timeline)                           # no timeline requested
+    refused(inv, e.last_timing)                               # timing off
+    refused(inv, e.upload, "output_norm.weight", 0, [shape.hidden], np.ones(shape.hidden, np.float32))
+    e.prefill(prompt, 0)
+    got = [e.select()]
+    refused(inv, e.step, got[0], ctx)                         # position outside the context
+    refused(inv, e.step, V, len(prompt))                      # token out of range
+    e.step_submit(got[0], len(prompt))
+    e.step_submit(-1, len(prompt) + 1)
+    refused(inv, e.step_submit, -1, len(prompt) + 2)          # two steps outstanding
+    refused(inv, e.read, capi.READ_HIDDEN)                    # state busy while steps are queued
+    got += [e.step_collect(), e.step_collect()]
+    for k in range(2, 5):
+        got.append(e.step(got[-1], len(prompt) + k))
+    assert got == want, (got, want)
+    e.close()
+
+    partial = capi.Engine(shape.gg_config())
+    refused(capi.GG_ERR_MISSING, partial.finalize)            # no tensors uploaded
+    partial.close()
