@@ -510,3 +510,48 @@ def test_invalid_calls_are_refused_and_leave_the_context_usable(gpu, tiny_model)
     partial = capi.Engine(shape.gg_config())
     refused(capi.GG_ERR_MISSING, partial.finalize)            # no tensors uploaded
     partial.close()
+
+
+def test_two_persistent_contexts_take_turns(gpu):
+    """Two contexts of one process on one device, each on the persistent
+    kernel, interleave their steps (sequential and pipelined, with steps of
+    both queued at once): their launches take turns, so neither times out
+    and falls back to the graph path, and each produces exactly the ids it
+    produces alone."""
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    ta, tb = synth.make_model(shape, seed=21), synth.make_model(shape, seed=22)
+    pa = synth.prompt_ids(30, seed=1, vocab=shape.vocab)
+    pb = synth.prompt_ids(45, seed=2, vocab=shape.vocab)
+
+    def alone(t, prompt):
+        e = engine(shape, t, prefill_batch=32)
+        e.prefill(prompt, 0)
+        ids = [e.select()]
+        for k in range(16):
+            ids.append(e.step(ids[-1], len(prompt) + k))
+        e.close()
+        return ids
+
+    want_a, want_b = alone(ta, pa), alone(tb, pb)
+    a, b = engine(shape, ta, prefill_batch=32), engine(shape, tb, prefill_batch=32)
+    assert a.decode_path() == b.decode_path() == "fused"
+    a.prefill(pa, 0)
+    b.prefill(pb, 0)
+    ga, gb = [a.select()], [b.select()]
+    for k in range(8):   # sequential, alternating
+        ga.append(a.step(ga[-1], len(pa) + k))
+        gb.append(b.step(gb[-1], len(pb) + k))
+    a.step_submit(ga[-1], len(pa) + 8)
+    b.step_submit(gb[-1], len(pb) + 8)
+    for k in range(9, 16):   # pipelined on both, one step of each queued ahead
+        a.step_submit(-1, len(pa) + k)
+        b.step_submit(-1, len(pb) + k)
+        ga.append(a.step_collect())
+        gb.append(b.step_collect())
+    ga.append(a.step_collect())
+    gb.append(b.step_collect())
+    assert a.decode_path() == b.decode_path() == "fused"
+    assert ga == want_a, (ga, want_a)
+    assert gb == want_b, (gb, want_b)
+    a.close()
+    b.close()
