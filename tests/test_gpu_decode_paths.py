@@ -555,3 +555,47 @@ def test_two_persistent_contexts_take_turns(gpu):
     assert gb == want_b, (gb, want_b)
     a.close()
     b.close()
+
+
+def test_two_persistent_contexts_from_two_threads(gpu):
+    """The same two contexts driven from two host threads at once (the
+    binding runs its calls on a thread pool; ctypes releases the GIL around
+    each C call): the process-wide ordering of persistent launches keeps
+    both on the persistent path, each with its solo ids, pipelined steps
+    included."""
+    import threading
+    shape = synth.GEMMA3_270M.with_ctx(1024).gemma3_mode()
+    models = [synth.make_model(shape, seed=31), synth.make_model(shape, seed=32)]
+    prompts = [synth.prompt_ids(37, seed=3, vocab=shape.vocab), synth.prompt_ids(52, seed=4, vocab=shape.vocab)]
+
+    def run(e, prompt, out):
+        e.prefill(prompt, 0)
+        ids = [e.select()]
+        for k in range(6):
+            ids.append(e.step(ids[-1], len(prompt) + k))
+        e.step_submit(ids[-1], len(prompt) + 6)
+        for k in range(7, 20):
+            e.step_submit(-1, len(prompt) + k)
+            ids.append(e.step_collect())
+        ids.append(e.step_collect())
+        out.append(ids)
+
+    want = []
+    for t, p in zip(models, prompts):
+        e = engine(shape, t, prefill_batch=32)
+        out = []
+        run(e, p, out)
+        e.close()
+        want.append(out[0])
+    engines = [engine(shape, t, prefill_batch=32) for t in models]
+    outs = [[], []]
+    threads = [threading.Thread(target=run, args=(engines[i], prompts[i], outs[i])) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads)
+    assert [e.decode_path() for e in engines] == ["fused", "fused"]
+    assert outs[0] == [want[0]] and outs[1] == [want[1]]
+    for e in engines:
+        e.close()
