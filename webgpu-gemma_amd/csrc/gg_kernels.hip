@@ -926,6 +926,17 @@ __device__ __forceinline__ void split4_bf16(float x0, float x1, float x2, float 
   lo = __builtin_bit_cast(bf16x4, l);
 }
 
+// max / sum with lane ^ 16 and lane ^ 32 on the gfx950 half-row and
+// half-wave swaps (VALU) instead of ds_bpermute shuffles (an LDS round trip)
+__device__ __forceinline__ float pf_xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pf_xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 constexpr int kPfRows = 32;   // query rows per block: two 16-row MFMA tiles
 __device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, *(const u32x4*)p);
@@ -1093,8 +1104,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_pf(AttnArgs a) {
             mx = fmaxf(mx, p[j][r]);
           }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = pf_xor32_max(pf_xor16_max(mx));
       const float mn = fmaxf(m, mx);
       const float mb = mn == -INFINITY ? 0.f : mn;   // a row with no key yet keeps p = 0
       alpha = __builtin_amdgcn_exp2f(m - mb);
