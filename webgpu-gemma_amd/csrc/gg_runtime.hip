@@ -535,20 +535,18 @@ int record_select(gg_ctx* c) { return record_select_impl(c, false); }
 int capture(gg_ctx* c, int (*rec)(gg_ctx*), hipGraphExec_t* out) {
   GG_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed));
   c->capturing = true;
+  c->probe_err = hipSuccess;   // direct launches' records are not this capture's
   int rc = rec(c);
   c->capturing = false;
   hipGraph_t g = nullptr;
   hipError_t e = hipStreamEndCapture(c->stream, &g);
-  if (rc != GG_OK) {
+  // a failed probe record belongs to this capture alone, whatever its outcome
+  const hipError_t pe = c->probe_err;
+  c->probe_err = hipSuccess;
+  if (rc != GG_OK || e != hipSuccess || pe != hipSuccess) {
     if (g) (void)hipGraphDestroy(g);
-    return rc;
-  }
-  if (e != hipSuccess) return hip_fail(c, e, "hipStreamEndCapture");
-  if (c->probe_err != hipSuccess) {
-    (void)hipGraphDestroy(g);
-    const hipError_t pe = c->probe_err;
-    c->probe_err = hipSuccess;
-    return hip_fail(c, pe, "probe event record");
+    if (rc != GG_OK) return rc;
+    return e != hipSuccess ? hip_fail(c, e, "hipStreamEndCapture") : hip_fail(c, pe, "probe event record");
   }
   e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
