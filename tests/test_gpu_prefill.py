@@ -102,6 +102,42 @@ def test_1b_batched_prefill_2048_matches_token_by_token(gpu, mode):
     b.close()
 
 
+def test_1b_batched_prefill_short_turns_match_token_by_token(gpu):
+    """Gemma-3-1B shapes, gemma3 attention: two short turns (300 prompt ids,
+    then 77 more at position 300) batched against the token-by-token path.
+    Row counts this small run the QKV, O and down GEMMs on 96-wide tiles
+    (K split in 2 and 4), the 2048-row prefill only its QKV GEMM."""
+    shape = synth.GEMMA3_1B.with_ctx(4096).gemma3_mode()
+    say("1b short batched turns, 300 + 77 ids")
+    if "1b" not in _MODELS:
+        _MODELS["1b"] = synth.make_model(shape, seed=1)
+    t = _MODELS["1b"]
+    first = synth.prompt_ids(300, seed=300, vocab=shape.vocab)
+    second = synth.prompt_ids(77, seed=77, vocab=shape.vocab)
+    a = engine(shape, t, 2048)
+    b = engine(shape, t, 0)
+    pos = 0
+    for ids in (first, second):
+        a.prefill(ids, pos)
+        b.prefill(ids, pos)
+        pos += len(ids)
+        for l in range(shape.layers):
+            assert rel(a.read(capi.READ_LAYER_HIDDEN, l), b.read(capi.READ_LAYER_HIDDEN, l)) < TOL, (pos, l)
+        for l in (0, 5, 25):
+            ka = a.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:pos]
+            kb = b.read(capi.READ_K_CACHE, l).reshape(shape.ctx, 256)[:pos]
+            assert rel(ka, kb) < TOL, (pos, l)
+        ta, tb = a.select(), b.select()
+        assert rel(a.read(capi.READ_LOGITS), b.read(capi.READ_LOGITS)) < TOL, pos
+        assert ta == tb, pos
+    for _ in range(4):
+        ta, tb = a.step(ta, pos), b.step(tb, pos)
+        assert ta == tb
+        pos += 1
+    a.close()
+    b.close()
+
+
 def test_1b_batched_prefill_ragged_slices_long_span(gpu):
     """Gemma-3-1B shapes at contextLength 8192, gemma3 attention: a 6000-id
     prompt prefilled in ragged batched slices (2500 + 2500 + 1000 rows: no

@@ -158,7 +158,7 @@ struct GemmArgs {
   const float* D;          // [N][K / 32]
   int M, N, K;
   int ks;                  // K slices (1..kGemmMaxSlices, EPI_OUT only): slice z covers K/ks and writes C + z M N
-  int bn;                  // block tile width: 128, or 144 (EPI_OUT, 4 waves of 32 x 144)
+  int bn;                  // block tile width: 128, or 144 / 96 (EPI_OUT: 4 waves of 32 x 144 / 64 x 48)
   float* C;                // EPI_OUT: [M][N] per slice
   uint16_t* act;           // EPI_GEGLU: hi plane [M][N/2], then lo plane; gate / up rows
                            // alternate in groups of 16 (16 gate rows, then their up rows)

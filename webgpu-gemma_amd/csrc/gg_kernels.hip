@@ -1259,10 +1259,11 @@ __global__ __launch_bounds__(256) void k_attn_pf_merge(AttnArgs a) {
 // with the block sum on the matrix cores.
 //
 // Block tile 128 (rows) x BN (features) x 64 (k step), four waves of
-// 16 NI x 16 NJ (NI x NJ MFMA tiles): 2 x 2 waves of 64 x 64 (BN = 128) or
+// 16 NI x 16 NJ (NI x NJ MFMA tiles): 2 x 2 waves of 64 x 64 (BN = 128),
 // 4 x 1 waves of 32 x 144 (BN = 144; 1152-wide outputs then split into 8
 // tiles, so that a K split of 4 fills the 512 block slots of the chip
-// exactly). LDS rows are padded to 72 bf16 so that the 16 lanes of a lane
+// exactly) or 2 x 2 waves of 64 x 48 (BN = 96; the 1536 QKV outputs in 16
+// tiles, so that a K split of 2 gives 512 blocks at 2048 rows). LDS rows are padded to 72 bf16 so that the 16 lanes of a lane
 // group (16 rows, one 16-byte chunk) cover all banks; the next step's global
 // loads are issued before the current step's MFMAs.
 // ---------------------------------------------------------------------------
@@ -1952,13 +1953,14 @@ int launch_dequant(const uint8_t* src, float* out, long long n, void* stream) {
 
 int launch_gemm(int epi, const GemmArgs& a, void* stream) {
   const int bn = a.bn;
-  if (a.M < 1 || (bn != 128 && bn != 144) || (bn == 144 && epi != EPI_OUT) || a.N < bn || a.N % bn ||
+  if (a.M < 1 || (bn != 128 && bn != 144 && bn != 96) || (bn != 128 && epi != EPI_OUT) || a.N < bn || a.N % bn ||
       a.K < 64 || a.ks < 1 || a.ks > kGemmMaxSlices || a.K % (64 * a.ks) || !a.A || !a.W || !a.D ||
       (epi == EPI_OUT ? !a.C : (!a.act || a.ks != 1)))
     return (int)hipErrorInvalidValue;
   dim3 grid(a.N / bn, (a.M + kGBM - 1) / kGBM, a.ks);
   if (epi == EPI_GEGLU) hipLaunchKernelGGL((k_gemm<EPI_GEGLU, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, a);
   else if (bn == 128) hipLaunchKernelGGL((k_gemm<EPI_OUT, 4, 4>), grid, dim3(256), 0, (hipStream_t)stream, a);
+  else if (bn == 96) hipLaunchKernelGGL((k_gemm<EPI_OUT, 4, 3>), grid, dim3(256), 0, (hipStream_t)stream, a);
   else hipLaunchKernelGGL((k_gemm<EPI_OUT, 2, 9>), grid, dim3(256), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }

@@ -637,28 +637,30 @@ int sync(gg_ctx* c, const char* what) {
 }
 
 
-// Block tile width (128, or 144 for a C output whose width it divides) and K
-// slices (up to max_ks, dividing K into whole 64-steps) that minimise the
-// modelled time, in units of one block's 64-wide step on a CU of its own:
+// Block tile width (128, or 144 or 96 for a C output whose width it divides)
+// and K slices (up to max_ks, dividing K into whole 64-steps) that minimise
+// the modelled time, in units of one block's 64-wide step on a CU of its own:
 // steps per block times the load of the busiest CU, where n >= 2 co-resident
 // blocks take 0.75 n of one block's time (measured on the 1B down GEMM: 144
 // blocks x 108 steps 165 us, 288 x 54 124 us), times 1.2 for the 144-wide
 // tile (1.125x the work per step; 85.5 us for 512 x 27 steps against 98.6 us
-// for 432 x 36 steps of the 128-wide tile), plus one unit per 2.29 M outputs
-// of each slice for the consumer's read of that slice (9.4 MB in ~1.9 us at
-// M = 2048, N = 1152). C must hold that many slices; the consumer adds them.
+// for 432 x 36 steps of the 128-wide tile) or 0.96 for the 96-wide one (the
+// 1B QKV GEMM, two blocks on the busiest CUs either way: 512 x 9 steps 24.7
+// us against 384 x 9 steps 25.7 us), plus one unit per 2.29 M outputs of each
+// slice for the consumer's read of that slice (9.4 MB in ~1.9 us at M = 2048,
+// N = 1152). C must hold that many slices; the consumer adds them.
 void gemm_plan(int N, int K, int M, int max_ks, bool out, int* bn_out, int* ks_out) {
   const int steps = K / 64;
   double best_cost = 0.0;
   *bn_out = 128;
   *ks_out = 1;
-  for (int bn : {128, 144}) {
-    if (N % bn || (bn == 144 && !out)) continue;
+  for (int bn : {128, 144, 96}) {
+    if (N % bn || (bn != 128 && !out)) continue;
     const int tiles = (N / bn) * ((M + 127) / 128);
     for (int ks = 1; ks <= max_ks; ++ks) {
       if (steps % ks) continue;
       const int per_cu = (tiles * ks + 255) / 256;
-      const double cost = (per_cu == 1 ? 1.0 : 0.75 * per_cu) * (steps / ks) * (bn == 144 ? 1.2 : 1.0) +
+      const double cost = (per_cu == 1 ? 1.0 : 0.75 * per_cu) * (steps / ks) * (bn == 144 ? 1.2 : bn == 96 ? 0.96 : 1.0) +
                           (out ? ks * ((double)M * N / 2.29e6) : 0.0);
       if ((bn == 128 && ks == 1) || cost < best_cost) {
         best_cost = cost;
