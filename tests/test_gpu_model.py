@@ -74,6 +74,51 @@ def test_tiny_greedy_loop(gpu, tiny_model, mode, path):
     e.close()
 
 
+@pytest.mark.parametrize("path", ["fused", "graph"])
+def test_tiny_context_filled_to_its_last_position(gpu, tiny_model, path):
+    """The last positions of the context: a batched prefill of ctx - 6 ids,
+    then greedy steps at ctx - 6 .. ctx - 1 (the last cache row) against the
+    oracle, every K/V row of the full cache compared; then, after a reset, one
+    batched prefill that ends exactly at ctx (engine.ts:923-928 allows
+    start + n == contextLength)."""
+    shape = synth.TINY.gemma3_mode(window=7)
+    ctx = shape.ctx
+    say("tiny context to its last position", path)
+    e = capi.Engine(shape.gg_config(prefill_batch=64))
+    e.set_decode_path(path)
+    e.upload_model(tiny_model)
+    e.finalize()
+    assert e.decode_path() == path
+    o = orc.OracleModel(shape, tiny_model)
+    prompt = synth.prompt_ids(ctx - 6, seed=13, vocab=shape.vocab)
+    e.prefill(prompt, 0)
+    o.prefill(prompt, 0)
+    tok = e.select(0.0, 0.9, 1.0, 0.0)
+    assert tok == o.select(0.0, 0.9, 1.0, 0.0)
+    pos = len(prompt)
+    while pos < ctx:
+        nxt = e.step(tok, pos, 0.0, 0.9, 1.0, 0.0)
+        o.forward(tok, pos)
+        ref = o.select(0.0, 0.9, 1.0, 0.0)   # the oracle's LM head runs in its select
+        check_state(e, o, shape, f"pos {pos}")
+        assert rel(e.read(capi.READ_LOGITS), o.buffer(orc.GOR_LOGITS)) < TOL, pos
+        assert nxt == ref, pos
+        tok, pos = nxt, pos + 1
+    for l in range(shape.layers):
+        assert rel(e.read(capi.READ_K_CACHE, l), o.buffer(orc.GOR_K_CACHE, l)) < TOL, l
+        assert rel(e.read(capi.READ_V_CACHE, l), o.buffer(orc.GOR_V_CACHE, l)) < TOL, l
+    with pytest.raises(capi.GGError):
+        e.step(tok, ctx)
+    full = synth.prompt_ids(ctx, seed=14, vocab=shape.vocab)
+    e.reset_kv()
+    e.prefill(full, 0)
+    o2 = orc.OracleModel(shape, tiny_model)
+    o2.prefill(full, 0)
+    check_state(e, o2, shape, "prefill to ctx")
+    assert e.select(0.0, 0.9, 1.0, 0.0) == o2.select(0.0, 0.9, 1.0, 0.0)
+    e.close()
+
+
 def test_prefill_equals_steps_and_turns(gpu, tiny_model):
     shape = synth.TINY.gemma3_mode(window=5)
     say("prefill vs steps")
