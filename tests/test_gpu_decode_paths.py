@@ -75,6 +75,19 @@ def test_sampled_steps_select_exactly_from_their_logits(gpu, path):
         assert nxt == want, (path, step, nxt, want)
         seen.add(nxt)
         tok, pos = nxt, pos + 1
+    # the ends of the draw and of the top-p cutoff: u = 0 and just below 1,
+    # top-p 1 (possibly all 256 candidates), a top-p below the first
+    # probability, a near-flat distribution at a high temperature
+    top = 1.0 - 2.0 ** -40
+    for T, top_p, rep, u in [(0.8, 0.9, 1.3, 0.0), (0.8, 0.9, 1.3, top), (0.8, 1.0, 1.3, float(rng.random())),
+                             (0.8, 1.0, 1.0, top), (0.8, 1e-6, 1.3, float(rng.random())),
+                             (50.0, 0.999, 1.3, float(rng.random())), (50.0, 1.0, 1.0, top)]:
+        nxt = e.step(tok, pos, T, top_p, rep, u)
+        vals, ids = orc.topk256(e.read(capi.READ_LOGITS))
+        want = orc.sample_candidates(vals, ids, sorted(seen), T, top_p, rep, u)
+        assert nxt == want, (path, T, top_p, rep, u, nxt, want)
+        seen.add(nxt)
+        tok, pos = nxt, pos + 1
     e.close()
 
 

@@ -135,3 +135,12 @@ def test_sampler_matches_host_semantics(gpu, seed):
         u = float(rng.random())
         tok, _, _ = _select(v, seen, T, p, rep, u)
         assert tok == orc.sample_candidates(vals, ids, seen, T, p, rep, u), (T, p, rep, u)
+    # the ends of the walk and of the top-p cutoff: draws at 0 and just below
+    # 1, top-p 1 (the cumulative sum may never reach it: all 256 candidates),
+    # a top-p below the first probability (one candidate), and a near-flat
+    # distribution at a high temperature (the longest walks)
+    for T, p, rep, u in [(0.7, 0.9, 1.0, 0.0), (0.7, 0.9, 1.0, 1.0 - 2.0 ** -40), (0.7, 1.0, 1.2, float(rng.random())),
+                         (0.7, 1.0, 1.0, 1.0 - 2.0 ** -40), (0.7, 1e-6, 1.0, float(rng.random())),
+                         (50.0, 0.999, 1.0, float(rng.random())), (50.0, 1.0, 1.0, 1.0 - 2.0 ** -40)]:
+        tok, _, _ = _select(v, seen, T, p, rep, u)
+        assert tok == orc.sample_candidates(vals, ids, seen, T, p, rep, u), (T, p, rep, u)
