@@ -246,8 +246,8 @@ struct SelShared {
   union {
     Cand ws[256];       // sampling: each wave's 64 candidates in sorted order
     struct {
-      float probs[256];
-      double pre[257];  // sampling: pre[k] = probs[0] + ... + probs[k - 1], summed in order
+      double pd[256];   // sampling: (double) of the f32 probability of rank k
+      double pre_g[17]; // sampling: pre_g[g] = pd[0] + ... + pd[16 g - 1], summed in order
     };
   };
   int tok;
@@ -361,54 +361,61 @@ static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, fl
   }
   __syncthreads();
   if (T == 0.0) return (int)sh.cs[0].id;
-  if (active) sh.probs[tid] = (float)exp((sh.cs[tid].val - sh.cs[0].val) / T);
+  if (active) sh.pd[tid] = (double)(float)exp((sh.cs[tid].val - sh.cs[0].val) / T);
   __syncthreads();
-  // thread 0's sequential passes read 16 values per LDS round trip (a
-  // load per step would wait out the LDS latency 256 times); within a group
-  // the same operations run in the same order, the exits become flags
+  // thread 0's sequential passes carry one dependent f64 add per element and
+  // nothing else: every sum is non-decreasing (terms >= 0), so a group of 16
+  // is searched for its first qualifying element only when the group's last
+  // sum qualifies (or is NaN); the prefix sums are kept per group and the one
+  // the walk needs is finished from its group's start in the same order
   constexpr int G = 16;
   if (tid == 0) {
     double s = 0.0;
-    for (int c = 0; c < 256; c += G) {
-      float pv[G];
 #pragma unroll
-      for (int k = 0; k < G; ++k) pv[k] = sh.probs[c + k];
+    for (int g = 0; g < 256 / G; ++g) {
+      sh.pre_g[g] = s;
 #pragma unroll
-      for (int k = 0; k < G; ++k) {
-        sh.pre[c + k] = s;
-        s += (double)pv[k];
-      }
+      for (int k = 0; k < G; ++k) s += sh.pd[G * g + k];
     }
-    sh.pre[256] = s;
+    sh.pre_g[256 / G] = s;
   }
   __syncthreads();
-  if (active) sh.q[tid] = (double)sh.probs[tid] / sh.pre[256];
+  if (active) sh.q[tid] = sh.pd[tid] / sh.pre_g[256 / G];
   __syncthreads();
   if (tid == 0) {
     double cum = 0.0;
     int cutoff = 256;
     for (int c = 0; c < 256 && cutoff == 256; c += G) {
-      double qv[G];
-#pragma unroll
-      for (int k = 0; k < G; ++k) qv[k] = sh.q[c + k];
+      double cs[G];
 #pragma unroll
       for (int k = 0; k < G; ++k) {
-        cum += qv[k];
-        cutoff = (cutoff == 256 && cum >= p.top_p) ? c + k + 1 : cutoff;
+        cum += sh.q[c + k];
+        cs[k] = cum;
+      }
+      if (!(cum < p.top_p)) {
+        int first = G;
+#pragma unroll
+        for (int k = G - 1; k >= 0; --k) first = cs[k] >= p.top_p ? k : first;
+        if (first < G) cutoff = c + first + 1;
       }
     }
-    double r = p.u * sh.pre[cutoff];
+    // prefix sum of the cutoff's candidates: pd[0] + ... + pd[cutoff - 1]
+    double pc = sh.pre_g[cutoff / G];
+    for (int k = cutoff & ~(G - 1); k < cutoff; ++k) pc += sh.pd[k];
+    // the walk: r after element k is r - pd[0] - ... - pd[k] in this order;
+    // the first k < cutoff where it reaches 0 is the pick
+    double r = p.u * pc;
     int pick = -1;
     for (int c = 0; c < cutoff && pick < 0; c += G) {
-      float pv[G];
-#pragma unroll
-      for (int k = 0; k < G; ++k) pv[k] = sh.probs[c + k];
+      double rs[G];
 #pragma unroll
       for (int k = 0; k < G; ++k) {
-        const bool on = (c + k < cutoff) & (pick < 0);
-        const double rn = r - (double)pv[k];
-        r = on ? rn : r;
-        pick = (on & (rn <= 0)) ? c + k : pick;
+        r -= sh.pd[c + k];
+        rs[k] = r;
+      }
+      if (!(r > 0)) {
+#pragma unroll
+        for (int k = G - 1; k >= 0; --k) pick = (c + k < cutoff && rs[k] <= 0) ? c + k : pick;
       }
     }
     if (pick < 0) pick = cutoff - 1;
