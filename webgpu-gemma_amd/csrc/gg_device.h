@@ -369,13 +369,24 @@ static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, fl
   // sum qualifies (or is NaN); the prefix sums are kept per group and the one
   // the walk needs is finished from its group's start in the same order
   constexpr int G = 16;
+  // (each group's reads are issued before the previous group's adds, so the
+  // LDS latency stays off the chains)
   if (tid == 0) {
-    double s = 0.0;
+    double s = 0.0, nx[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) nx[k] = sh.pd[k];
 #pragma unroll
     for (int g = 0; g < 256 / G; ++g) {
+      double cur[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) cur[k] = nx[k];
+      if (g + 1 < 256 / G) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) nx[k] = sh.pd[G * (g + 1) + k];
+      }
       sh.pre_g[g] = s;
 #pragma unroll
-      for (int k = 0; k < G; ++k) s += sh.pd[G * g + k];
+      for (int k = 0; k < G; ++k) s += cur[k];
     }
     sh.pre_g[256 / G] = s;
   }
@@ -383,13 +394,20 @@ static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, fl
   if (active) sh.q[tid] = sh.pd[tid] / sh.pre_g[256 / G];
   __syncthreads();
   if (tid == 0) {
-    double cum = 0.0;
+    double cum = 0.0, nx[G];
     int cutoff = 256;
+#pragma unroll
+    for (int k = 0; k < G; ++k) nx[k] = sh.q[k];
     for (int c = 0; c < 256 && cutoff == 256; c += G) {
       double cs[G];
 #pragma unroll
+      for (int k = 0; k < G; ++k) cs[k] = nx[k];
+      const int cn = min(c + G, 256 - G);
+#pragma unroll
+      for (int k = 0; k < G; ++k) nx[k] = sh.q[cn + k];
+#pragma unroll
       for (int k = 0; k < G; ++k) {
-        cum += sh.q[c + k];
+        cum += cs[k];
         cs[k] = cum;
       }
       if (!(cum < p.top_p)) {
@@ -406,11 +424,18 @@ static __device__ __attribute__((noinline)) int select_sampled(SelShared& sh, fl
     // the first k < cutoff where it reaches 0 is the pick
     double r = p.u * pc;
     int pick = -1;
+#pragma unroll
+    for (int k = 0; k < G; ++k) nx[k] = sh.pd[k];
     for (int c = 0; c < cutoff && pick < 0; c += G) {
       double rs[G];
 #pragma unroll
+      for (int k = 0; k < G; ++k) rs[k] = nx[k];
+      const int cn = min(c + G, 256 - G);
+#pragma unroll
+      for (int k = 0; k < G; ++k) nx[k] = sh.pd[cn + k];
+#pragma unroll
       for (int k = 0; k < G; ++k) {
-        r -= sh.pd[c + k];
+        r -= rs[k];
         rs[k] = r;
       }
       if (!(r > 0)) {
