@@ -130,7 +130,9 @@ int gg_step(gg_ctx* ctx, int32_t token, int32_t pos, const gg_sample* s, double 
  * id that the previously submitted step (or the last gg_step / gg_select)
  * selects, read on the device, so the step can be queued before that id
  * reaches the host. gg_step_collect waits for the oldest submitted step and
- * returns its id.
+ * returns its id; on the persistent kernel's path it waits by polling the
+ * mapped host word the launch stores the id into (the calling thread spins;
+ * no event sits between the queued launches).
  *
  * At most two steps may be outstanding. Every other call except
  * gg_destroy fails with GG_ERR_INVALID while any is. A step that is

@@ -1544,7 +1544,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void k_decode(DecodeArgs a) {
                          : select_greedy(S.sel, m, id, tid < 256);
   if (tid == 0) {
     a.st->out_token = tok;
-    a.host_out[a.out_slot] = tok;
+    // system scope: the host polls this mapped word for the id of a queued step
+    __hip_atomic_store(a.host_out + a.out_slot, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     if (tok >= 0 && tok < a.V) {
       // no-return atomic OR: no load round trip at the end of the launch
       __hip_atomic_fetch_or(a.seen + (tok >> 5), 1u << (tok & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

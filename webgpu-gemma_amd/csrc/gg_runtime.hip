@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -144,7 +145,6 @@ struct gg_ctx {
   int pipe_n = 0, pipe_head = 0;      // outstanding steps, slot of the oldest
   bool pipe_launched[2] = {false, false};   // slot's step is a launch in flight (else its id is known)
   int32_t pipe_tok[2] = {0, 0};       // ids of steps that ran synchronously
-  hipEvent_t pipe_ev[2] = {nullptr, nullptr};
   struct PipeArgs { int32_t token, pos; gg_sample s; double u; };
   PipeArgs pipe_args[2] = {};         // each outstanding step's arguments (re-run after a fallback)
   bool have_prev = false;             // a selection has run: a step may take its id on the device
@@ -352,6 +352,7 @@ int persistent_end(gg_ctx* c) {
 // path (one kernel per phase, nothing to keep resident); the caller re-runs
 // the work. Returns kRetry after that switch, GG_OK when no flag is raised.
 constexpr int kRetry = 1;
+constexpr int32_t kNoId = (int32_t)0x80000000;   // a queued step's id word before the launch stores it
 int fall_back_to_graphs(gg_ctx* c) {
   GG_TRY(sync(c, "persistent decode kernel"));
   for (int i : {1, 8, 12, 13}) c->h_out[i] = 0;
@@ -1100,7 +1101,6 @@ int gg_finalize(gg_ctx* c) {
   for (int i = 0; i < 3; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->ev[i], hipEventDisableSystemFence));
   // completion of pipelined steps: the host reads each step's id from mapped
   // memory after its event, so these keep the system-scope release
-  for (int i = 0; i < 2; ++i) GG_HIP(c, hipEventCreateWithFlags(&c->pipe_ev[i], hipEventDisableTiming));
   if (c->probe_kind != GG_PROBE_NONE)
     // timing-only events: no system-scope fence (cache write-back/invalidate)
     // around the bracketed launch
@@ -1361,6 +1361,27 @@ int gg_step(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u,
   return step_impl(c, token, pos, s, u, out_token);
 }
 
+// A queued persistent step stores its id (or raises its timeout flag) in
+// mapped host memory; the host waits for either with plain loads. No runtime
+// call in the normal wait: a stream query or event wait would put a marker
+// between the queued launches. Past 100 ms the stream is queried, so a
+// launch that ended without an id, or a device error, is reported.
+int wait_step_id(gg_ctx* c, int slot) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (unsigned n = 1;; ++n) {
+    if (__atomic_load_n(&c->h_out[4 + slot], __ATOMIC_ACQUIRE) != kNoId ||
+        __atomic_load_n(&c->h_out[12 + slot], __ATOMIC_ACQUIRE) != 0)
+      return GG_OK;
+    if ((n & 4095) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(100)) {
+      const hipError_t q = hipStreamQuery(c->stream);
+      if (q != hipSuccess && q != hipErrorNotReady) return hip_fail(c, q, "persistent decode kernel");
+      if (q == hipSuccess && __atomic_load_n(&c->h_out[4 + slot], __ATOMIC_ACQUIRE) == kNoId &&
+          __atomic_load_n(&c->h_out[12 + slot], __ATOMIC_ACQUIRE) == 0)
+        return set_err(c, GG_ERR_HIP, "persistent decode kernel ended without an id");
+    }
+  }
+}
+
 int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, double u) {
   GG_TRY(check_ready(c));
   if (!s) return set_err(c, GG_ERR_INVALID, "null argument");
@@ -1383,8 +1404,11 @@ int gg_step_submit(gg_ctx* c, int32_t token, int32_t pos, const gg_sample* s, do
     a.in_rep_penalty = s->rep_penalty;
     a.in_u = u;
     a.out_slot = 4 + slot;
+    // the launch stores its id into this mapped word; no event is recorded
+    // behind it (a record between two queued launches idles the GPU ~6 us at
+    // every launch boundary)
+    __atomic_store_n(&c->h_out[4 + slot], kNoId, __ATOMIC_RELEASE);
     GG_TRY(launch_rc(c, launch_decode(DEC_STEP, a, c->stream, c->coop), "persistent decode kernel"));
-    GG_HIP(c, hipEventRecord(c->pipe_ev[slot], c->stream));
     GG_TRY(persistent_end(c));
     c->pipe_args[slot] = {token, pos, *s, u};
     c->pipe_launched[slot] = true;
@@ -1411,7 +1435,7 @@ int gg_step_collect(gg_ctx* c, int32_t* out_token) {
   c->pipe_head ^= 1;
   c->pipe_n -= 1;
   if (c->pipe_launched[slot]) {
-    GG_HIP(c, hipEventSynchronize(c->pipe_ev[slot]));
+    GG_TRY(wait_step_id(c, slot));
     if (c->h_out[12 + slot] != 0) {
       // this step's launch timed out, and a step queued behind it took its
       // id on the device: switch to the graph path and run both again there
@@ -1594,8 +1618,6 @@ void gg_destroy(gg_ctx* c) {
   for (hipEvent_t e : c->ev)
     if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->probe_ev)
-    if (e) (void)hipEventDestroy(e);
-  for (hipEvent_t e : c->pipe_ev)
     if (e) (void)hipEventDestroy(e);
   for (void* p : c->allocs) (void)hipFree(p);
   if (c->staging) (void)hipFree(c->staging);
